@@ -1,0 +1,158 @@
+/* tbf16_hip.h -- C ABI of the MI355X (gfx950) scaled-fp16 hot path.
+ *
+ * Drop-in boundary for tech-cosmos/turing-bf16's native extensions: every entry
+ * point below replaces one pybind11 export of tbf16/csrc/{gemm_sm75,small_kernels}.cu (or a third-party
+ * kernel the reference calls through torch), with the same argument meaning.
+ * Reference citations are paths relative to the reference tree.
+ *
+ * Conventions
+ *  - All tensor arguments are device pointers; shapes, strides (in elements) and
+ *    the HIP stream (hipStream_t passed as void*) are plain integers/pointers.
+ *  - The caller allocates every output and workspace; the library allocates
+ *    nothing. Launches are asynchronous on `stream`; nothing synchronizes.
+ *  - Return 0 on success, a negative TBF16_E* code on failure; the message is in
+ *    tbf16_last_error() (thread-local). Preconditions are checked on the host
+ *    before any launch, with the reference's messages where it has one.
+ *  - Scale exponents are exchanged as int32 p (scale = 2^p); inverse scales as
+ *    fp32 (2^-p), which is what the reference's Python API returns.
+ */
+#ifndef TBF16_HIP_H
+#define TBF16_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TBF16_ABI_VERSION 1
+
+#define TBF16_OK 0
+#define TBF16_EINVAL (-1) /* bad shape, stride, alignment or dtype */
+#define TBF16_ELAUNCH (-2) /* a HIP launch failed */
+#define TBF16_EWS (-3)    /* workspace too small */
+
+#define TBF16_DT_BF16 0
+#define TBF16_DT_F16 1
+
+/* Library identity. */
+int tbf16_abi_version(void);
+const char* tbf16_last_error(void);
+
+/* Per-row scale exponents p[r] (scale 2^p puts max|x[r,:]|, or the L1 norm with
+ * l1 != 0, in [2^(t-1), 2^t)); optional fp32 inverse scales 2^-p.
+ * Replaces row_scale (tbf16/csrc/gemm_sm75.cu:243-253, kernel :27-47). x bf16
+ * (M, K) row stride ldx; K % 8 == 0, ldx % 8 == 0, 16-byte aligned. */
+int tbf16_row_exps(const void* x, int64_t M, int64_t K, int64_t ldx, int t, int l1, int32_t* exps,
+                   float* s_inv, void* stream);
+
+/* y16 = fp16(x * 2^p[r]) and s_inv[r] = 2^-p[r].
+ * Replaces quantize_rows (tbf16/csrc/small_kernels.cu:275-287, kernel :35-74;
+ * Python tbf16/ops.py:85-100). */
+int tbf16_quantize_rows(const void* x, int64_t R, int64_t K, int64_t ldx, int t, int l1, void* y16, int64_t ldy,
+                        float* s_inv, void* stream);
+
+/* quantize_rows with the fp16 result written transposed: yT (K, R), row stride
+ * ldyT >= R. Same exponents as tbf16_quantize_rows with l1 = 0. exps_ws: int32
+ * (R,) workspace. Serves ScaledLinearFn.forward's saved x16 (tbf16/autograd.py:
+ * 62-65) in the layout dW consumes. */
+int tbf16_quantize_rows_t(const void* x, int64_t R, int64_t K, int64_t ldx, int t, void* yT, int64_t ldyT,
+                          float* s_inv, int32_t* exps_ws, void* stream);
+
+/* Column quantisation: amax[c] = max_r |x[r,c] * row_mul[r]|, y = fp16((x * row_mul)
+ * * 2^p[c]), s_inv[c] = 2^-p[c]; row_mul (R,) fp32 powers of two or NULL. The fp16
+ * result is written transposed: yT (K, R), row stride ldyT >= R.
+ * Replaces quantize_cols (tbf16/csrc/small_kernels.cu:318-340, kernels :136-184;
+ * Python tbf16/autograd.py:26-36). ws: tbf16_quantize_cols_ws_bytes(R, K) bytes. */
+size_t tbf16_quantize_cols_ws_bytes(int64_t R, int64_t K);
+int tbf16_quantize_cols_t(const void* x, int64_t R, int64_t K, int64_t ldx, int t, const float* row_mul, void* yT,
+                          int64_t ldyT, float* s_inv, void* ws, int64_t ws_bytes, void* stream);
+
+/* Fused scaled linear: y = bf16((sum_k fp16(x[m,k] * 2^p[m]) * w16[n,k]) * 2^-p[m]
+ * * ws[n] + bias[n]), fp16 MFMA with fp32 accumulation, p from tbf16_row_exps(x, t,
+ * l1) computed inside this call into exps_ws (int32 (M,)). One bf16 rounding.
+ * x bf16 (M, K); w16 fp16 (N, K); ws fp32 (N,); bias bf16 (N,) or NULL; y bf16
+ * (M, N). cfg < 0 picks the tile shape. Replaces linear (tbf16/csrc/gemm_sm75.cu:
+ * 257-284) and, at 2 <= M < 256, quantize_rows + cuBLAS + epilogue
+ * (tbf16/ops.py:174-189) without its fp16 intermediate. */
+int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N, int64_t ldw,
+                 const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg, int32_t* exps_ws,
+                 void* stream);
+
+/* tbf16_linear with the row exponents already computed (exps int32 (M,), e.g. by
+ * tbf16_quantize_rows_t): the training forward, which quantises x once for the
+ * saved fp16 copy and for the GEMM (tbf16/autograd.py:60-68). */
+int tbf16_linear_exps(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t* exps, const void* w16,
+                      int64_t N, int64_t ldw, const float* ws, const void* bias, void* y, int64_t ldy, int cfg,
+                      void* stream);
+
+/* GEMM on already-quantised fp16 operands, both K-contiguous:
+ * y = bf16((a16 @ b16^T) * sa[m] * sb[n] + bias[n]) with fp32 accumulation.
+ * Replaces the cuBLAS fp16 GEMM + epilogue pair of linear_q (tbf16/ops.py:178-189,
+ * small_kernels.cu:289-302) and _scaled_mm (tbf16/autograd.py:49-55). */
+int tbf16_gemm_f16(const void* a16, int64_t M, int64_t K, int64_t lda, const float* sa, const void* b16, int64_t N,
+                   int64_t ldb, const float* sb, const void* bias, void* y, int64_t ldy, int cfg, void* stream);
+
+/* M = 1: y[n] = bf16((sum_k x[k] * w16[n,k]) * ws[n] + bias[n]) in fp32.
+ * Replaces gemv (tbf16/csrc/small_kernels.cu:304-315, kernel :107-132). */
+int tbf16_gemv(const void* x, const void* w16, int64_t N, int64_t K, int64_t ldw, const float* ws, const void* bias,
+               void* y, void* stream);
+
+/* Per-(b, h) max |x| over (S, D) into out fp32 (B, H). x (B, H, S, D) bf16 or fp16
+ * with element strides (sb, sh, ss), contiguous D % 8 == 0.
+ * Replaces head_amax (tbf16/csrc/small_kernels.cu:342-359, kernel :222-243). */
+int tbf16_head_amax(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb, int64_t sh,
+                    int64_t ss, float* out, void* stream);
+
+/* y (contiguous B, H, S, D) = cast(x * 2^e[b, h]); e int32 with element strides
+ * (e_sb, e_sh) so that broadcast exponents need no copy.
+ * Replaces head_scale_cast (tbf16/csrc/small_kernels.cu:361-379, kernel :246-263). */
+int tbf16_head_scale_cast(const void* x, int in_dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                          int64_t sh, int64_t ss, const int32_t* e, int64_t e_sb, int64_t e_sh, void* y,
+                          int out_dtype, void* stream);
+
+/* Scaled attention forward (flash-style, no S x S buffer).
+ * Exponents (tbf16/attention.py:267-277): eq/ek = max over heads of frexp(amax),
+ * a = clamp(floor((ek - eq) / 2)), ev[b, hkv] = frexp(amax v[b, hkv]) - v_exp.
+ * Computes softmax((q 2^a)(k 2^-a)^T * scale + bias) (v 2^-ev) on fp16 MFMA with
+ * fp32 online softmax and writes o = bf16(O / l * 2^ev) once.
+ * q (B, H, Sq, D), k/v (B, Hkv, Sk, D) bf16, strides in elements (b, h, s) with
+ * contiguous D; D % 8 == 0, D <= 256; H % Hkv == 0. bias: optional fp16 additive
+ * mask read at bias[b*bsb + h*bsh + i*bsq + j] (strides may be 0 to broadcast).
+ * causal: key j visible to query i iff j <= i (top-left, as torch).
+ * Outputs: o bf16 (B, H, Sq, D) contiguous; optional lse fp32 (B, H, Sq) in log2
+ * units of (logit * scale * log2(e)); optional o16 fp16 (B, H, Sq, D) = O / l
+ * (saved for the backward); optional exps int32 [2 + B*Hkv] = {a, 0, ev...}.
+ * Replaces prepare_qkv + torch's fp16 memory-efficient SDPA + head_scale
+ * (tbf16/attention.py:285-294) and _eff_fwd (tbf16/autograd.py:155-164). */
+size_t tbf16_attn_fwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);
+int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t Hkv, int64_t Sq,
+                   int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const void* bias, const int64_t* bias_strides, float scale, int causal,
+                   int v_exp, void* o, float* lse, void* o16, int32_t* exps, void* ws, int64_t ws_bytes,
+                   void* stream);
+
+/* Scaled attention backward for one value of the dO target exponent t_do.
+ * e = max(frexp(amax dout[b,h]) + ev_q[b,h]), G = t_do - e, dO16 = fp16(dout *
+ * 2^(ev_q + G)). dq = bf16(scale * dS K16 * 2^(a-G)), dk = bf16(scale * sum_grp
+ * dS^T Q16 * 2^(-a-G)), dv = bf16(sum_grp P^T dO16 * 2^(-ev-G)), all from fp32.
+ * *overflow is set to 1 (device int, caller zeroes it) when any gradient in the
+ * scaled fp16 domain would overflow fp16 (|x| >= 65520) or is not finite, which
+ * is the reference's retry condition (tbf16/autograd.py:177-189). exps_out int32
+ * [2] = {e, G}. Inputs are the forward's q, k, v, o16, lse and exps.
+ * Replaces torch's _scaled_dot_product_efficient_attention_backward call and the
+ * surrounding scaling (tbf16/autograd.py:166-193). */
+size_t tbf16_attn_bwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);
+int tbf16_attn_bwd(const void* q, const void* k, const void* v, const void* o16, const float* lse,
+                   const void* dout, const int32_t* exps_fwd, int64_t B, int64_t H, int64_t Hkv, int64_t Sq,
+                   int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const int64_t* do_strides, const void* bias,
+                   const int64_t* bias_strides, float scale, int causal, int t_do, void* dq, void* dk, void* dv,
+                   int32_t* exps_out, int32_t* overflow, void* ws, int64_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TBF16_HIP_H */

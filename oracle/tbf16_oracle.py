@@ -1,0 +1,434 @@
+"""CPU restatement of tbf16's scaled-fp16 hot path.
+
+TEST INFRASTRUCTURE ONLY. This module is the checker for the HIP kernels: only
+`tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may
+import it. The product package (`turing-bf16_amd/tbf16`) never imports it and has
+no CPU fallback.
+
+Every function cites the reference line it restates (paths relative to the
+tech-cosmos/turing-bf16 tree). Bit-level parts (exponents, fp16/bf16 payloads) are
+exact; floating-point GEMM/attention parts run in fp32 (the reference's
+accumulation type) or fp64 (the accuracy reference the reference's tests use).
+
+How each function is pinned (checked by tests/test_oracle.py):
+  pow2_exp / pow2_exp_fused   closed-form invariant amax*2^p in [2^(t-1), 2^t) for
+                              every normal bf16 amax, frexp identity, edge table,
+                              the C restatement (oracle/pow2.c) and the golden KAT.
+  quantize_rows/quantize_cols payload == torch's RNE float->half of the same fp32
+                              product; s_inv*scale == 1; brute force on tiny inputs.
+  bf16/fp16 rounding          torch CPU RNE casts (library routines) and pow2.c.
+  linear_fused / gemv /       fp64 matmul of the same bf16 values (rel err bound),
+  linear_cublas_path          exact small-integer cases where fp32 is exact.
+  attn_exponents / head_exp   torch.frexp on amax; brute-force loop over heads.
+  sdpa_ref64 / attn_*         closed forms: q=0 -> prefix mean of V rows, one-hot
+                              logits copy a V row; fp64 autograd for gradients.
+  attn_bwd_exponents / retry  closed form of autograd.py:175-189 with an injected
+                              overflowing backward.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+FP16_MAX = 65504.0
+# Smallest |x| that rounds to inf in fp16 (round-to-nearest-even).
+FP16_OVERFLOW = 65520.0
+
+
+# ---------------------------------------------------------------------------
+# A1 / A2: power-of-two exponents (integer arithmetic on fp32 exponent bits)
+# ---------------------------------------------------------------------------
+
+def exp_field(amax) -> np.ndarray:
+    """Biased fp32 exponent field (bits >> 23) & 0xFF of float32 values."""
+    a = np.ascontiguousarray(np.asarray(amax, dtype=np.float32))
+    return ((a.view(np.int32) >> 23) & 0xFF).astype(np.int64)
+
+
+def pow2_exp(amax, t: int) -> np.ndarray:
+    """Scale exponent p (scale s = 2**p) of the small kernels' pow2_scale.
+
+    Restates tbf16/csrc/small_kernels.cu:12-18: e = clamp(E(amax), 1, 252),
+    se = clamp(126 + t - (e - 127), 1, 254), s = 2**(se - 127). For a normal amax
+    this puts amax * s in [2**(t-1), 2**t). Used by quantize_rows / quantize_cols
+    (small_kernels.cu:61,172) and so by prepare_weight and the training ops.
+    """
+    e = np.clip(exp_field(amax), 1, 252)
+    se = np.clip(253 + t - e, 1, 254)
+    return (se - 127).astype(np.int32)
+
+
+def pow2_exp_fused(amax, t: int) -> np.ndarray:
+    """Fused GEMM row_scale variant, tbf16/csrc/gemm_sm75.cu:19-23: only the upper
+    clamp on the biased scale exponent. Identical to pow2_exp for t >= 2 (the fused
+    path always uses t = 15, tbf16/ops.py:37)."""
+    e = np.clip(exp_field(amax), 1, 252)
+    se = np.minimum(253 + t - e, 254)
+    return (se - 127).astype(np.int32)
+
+
+def pow2_exp_triton(amax, t: int) -> np.ndarray:
+    """Triton fallback variant, tbf16/ops.py:50-56,68,77: 2**(126 - e) * 2**t with
+    no clamp of the result. Returned as an exponent that may exceed 127 (the
+    reference then holds inf). Kept only to document where the variants differ."""
+    e = np.clip(exp_field(amax), 1, 252)
+    return (126 - e + t).astype(np.int32)
+
+
+def frexp_exp(v) -> np.ndarray:
+    """torch.frexp exponent (v = m * 2**e, m in [0.5, 1); 0 for 0, inf, nan)."""
+    m, e = np.frexp(np.asarray(v, dtype=np.float32))
+    e = np.where(np.isfinite(np.asarray(v, dtype=np.float32)), e, 0)
+    return e.astype(np.int32)
+
+
+def target_exp(K: int) -> int:
+    """tbf16/ops.py:40-43: rows scaled to amax in [2^(t-1), 2^t) keep |C| < K*4^t."""
+    return min(0, (15 - math.ceil(math.log2(max(K, 1)))) // 2)
+
+
+def dw_target_exp(M: int) -> int:
+    """tbf16/autograd.py:85: |dW16| < M * 2^t must stay under fp16's max."""
+    return min(0, 15 - math.ceil(math.log2(max(M, 1))))
+
+
+def attn_do_target(D: int) -> int:
+    """tbf16/autograd.py:176: t_do = 12 - ceil(log2 D)."""
+    return 12 - math.ceil(math.log2(D))
+
+
+L1_TARGET = 15            # tbf16/ops.py:141
+FUSED_T = 15              # tbf16/ops.py:37
+FUSED_MIN_M = 256         # tbf16/ops.py:34
+SMALL_M = 2               # tbf16/ops.py:215
+
+
+def ldexp1(p) -> np.ndarray:
+    """float32 2**p (exact; 2**-127 is an fp32 subnormal and stays one)."""
+    return np.ldexp(np.float32(1.0), np.asarray(p, dtype=np.int32)).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Rounding helpers (bit-level, independent of torch's casts)
+# ---------------------------------------------------------------------------
+
+def bf16_bits_to_f32(bits) -> np.ndarray:
+    b = np.asarray(bits, dtype=np.uint32) << 16
+    return b.view(np.float32)
+
+
+def f32_to_bf16_rne_bits(x) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN."""
+    u = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32).astype(np.uint64)
+    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    r = np.where(nan, (u >> 16) | 0x40, r)
+    return r.astype(np.uint16)
+
+
+# ---------------------------------------------------------------------------
+# a2 / a4 / a5 / a9: row and column quantisation
+# ---------------------------------------------------------------------------
+
+def row_amax(x: torch.Tensor, l1: bool) -> np.ndarray:
+    """Per-row max |x| (exact) or L1 norm. The L1 norm is the exact sum rounded
+    once to fp32; the reference sums in fp32 in thread order
+    (small_kernels.cu:42-59), which can differ only when the sum lies within an
+    fp32 ulp of a power of two."""
+    xf = x.float()
+    if l1:
+        return xf.double().abs().sum(1).float().numpy()
+    if xf.shape[1] == 0:
+        return np.zeros(xf.shape[0], np.float32)
+    # fmaxf in the reference's reduction skips NaN operands (small_kernels.cu:48)
+    return torch.nan_to_num(xf.abs(), nan=0.0).amax(1).numpy()
+
+
+def row_exps(x: torch.Tensor, t: int, l1: bool = False, fused: bool = False) -> np.ndarray:
+    """Row scale exponents: quantize_rows (small_kernels.cu:35-74) or the fused
+    GEMM's row_scale (gemm_sm75.cu:27-47)."""
+    amax = row_amax(x, l1)
+    return pow2_exp_fused(amax, t) if fused else pow2_exp(amax, t)
+
+
+def quantize_rows(x: torch.Tensor, t: int = 0, l1: bool = False):
+    """bf16 (R, K) -> (fp16 (R, K), fp32 s_inv (R,)).
+
+    Restates quantize_rows (tbf16/ops.py:85-100 -> small_kernels.cu:35-74):
+    y = fp16_rne(x * s) with s = 2**p from pow2_exp, s_inv = 1 / s.
+    """
+    p = row_exps(x, t, l1)
+    s = torch.from_numpy(ldexp1(p))
+    y = (x.float() * s[:, None]).half()
+    return y, torch.from_numpy(ldexp1(-p))
+
+
+def prepare_weight(w: torch.Tensor):
+    """tbf16/ops.py:151-153: quantize_rows(w, target_exp(K))."""
+    return quantize_rows(w.contiguous(), target_exp(w.shape[1]))
+
+
+def quantize_cols(x: torch.Tensor, t: int = 0, row_mul: torch.Tensor | None = None):
+    """bf16 (R, K) -> (fp16 (R, K), fp32 s_inv (K,)), one scale per column.
+
+    Restates col_amax_kernel + col_convert_kernel (small_kernels.cu:136-184,
+    318-340): amax[c] = max_r |x[r,c]| * |row_mul[r]|, y = fp16((x * row_mul) * s_c).
+    R == 0 gives s_inv = 1 (small_kernels.cu:325).
+    """
+    R, K = x.shape
+    if R == 0:
+        return torch.empty(0, K, dtype=torch.float16), torch.ones(K)
+    xf = x.float()
+    rm = row_mul.float() if row_mul is not None else torch.ones(R)
+    amax = (xf.abs() * rm.abs()[:, None]).amax(0).numpy()
+    p = pow2_exp(amax, t)
+    s = torch.from_numpy(ldexp1(p))
+    y = ((xf * rm[:, None]) * s[None, :]).half()
+    return y, torch.from_numpy(ldexp1(-p))
+
+
+# ---------------------------------------------------------------------------
+# a3 / a6 / a7 / a8: linear
+# ---------------------------------------------------------------------------
+
+def _epilogue(acc: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor, bias) -> torch.Tensor:
+    """acc * sa[m] * sb[n] + bias[n] in fp32, one RNE rounding to bf16
+    (gemm_sm75.cu:215-216, small_kernels.cu:94-99)."""
+    y = acc.float() * sa.float()[:, None] * sb.float()[None, :]
+    if bias is not None:
+        y = y + bias.float()[None, :]
+    return y.bfloat16()
+
+
+def linear_fused(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None, t: int = FUSED_T,
+                 l1: bool = False) -> torch.Tensor:
+    """Fused GEMM (gemm_sm75.cu:78-226, 257-284): x rows scaled (row_scale),
+    converted to fp16, fp32 accumulation, bf16 out from fp32 (single rounding)."""
+    p = row_exps(x, t, l1, fused=not l1)
+    x16 = (x.float() * torch.from_numpy(ldexp1(p))[:, None]).half()
+    acc = x16.float() @ w16.float().t()
+    return _epilogue(acc, torch.from_numpy(ldexp1(-p)), ws, bias)
+
+
+def linear_cublas_path(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None) -> torch.Tensor:
+    """The reference's 2 <= M < 256 regime (ops.py:174-189): L1 row scales at
+    t = 15, an fp16 C (cuBLAS fp16 output) and then the bf16 epilogue. This double
+    rounding is the reference's own error at small M."""
+    x16, sx = quantize_rows(x, L1_TARGET, l1=True)
+    c16 = (x16.float() @ w16.float().t()).half()
+    return _epilogue(c16.float(), sx, ws, bias)
+
+
+def linear_small_m(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None) -> torch.Tensor:
+    """This build's 2 <= M < 256 path: the reference's L1 exponents (ops.py:174)
+    with fp32 accumulation and a single bf16 rounding (no fp16 C)."""
+    x16, sx = quantize_rows(x, L1_TARGET, l1=True)
+    acc = x16.float() @ w16.float().t()
+    return _epilogue(acc, sx, ws, bias)
+
+
+def gemv(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None) -> torch.Tensor:
+    """M = 1 (small_kernels.cu:107-132): fp32 dot of bf16 x with fp16 w, times
+    ws, plus bias, one bf16 rounding. No activation scale."""
+    acc = x.float().reshape(1, -1) @ w16.float().t()
+    y = acc * ws.float()[None, :]
+    if bias is not None:
+        y = y + bias.float()[None, :]
+    return y.bfloat16()
+
+
+def scaled_linear(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None) -> torch.Tensor:
+    """Dispatcher of tbf16/ops.py:164-175 as this build runs it: M < 2 -> GEMV,
+    M >= 256 -> fused (max rows, t = 15), else L1 rows at t = 15; all with fp32
+    accumulation and one bf16 rounding."""
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    M = x2.shape[0]
+    if M < SMALL_M:
+        y = gemv(x2, w16, ws, bias) if M == 1 else torch.empty(0, w16.shape[0], dtype=torch.bfloat16)
+    elif M >= FUSED_MIN_M:
+        y = linear_fused(x2, w16, ws, bias)
+    else:
+        y = linear_small_m(x2, w16, ws, bias)
+    return y.reshape(*shape[:-1], w16.shape[0])
+
+
+def linear_ref64(x, w, bias=None) -> torch.Tensor:
+    """fp64 reference of the same bf16 values (tests/test_ops.py:13)."""
+    y = x.double() @ w.double().t()
+    return y + bias.double() if bias is not None else y
+
+
+# ---------------------------------------------------------------------------
+# a10: training linear (autograd.py:58-90)
+# ---------------------------------------------------------------------------
+
+def linear_train_fwd(x2: torch.Tensor, w: torch.Tensor, bias=None, double_round: bool = False):
+    """ScaledLinearFn.forward (autograd.py:60-68): x rows max-scaled at
+    target_exp(K), w via prepare_weight, fp32 accumulation (double_round: the
+    reference's fp16 GEMM output). Returns (y, x16, sx, w16, sw)."""
+    K = w.shape[1]
+    x16, sx = quantize_rows(x2, target_exp(K))
+    w16, sw = prepare_weight(w)
+    acc = x16.float() @ w16.float().t()
+    if double_round:
+        acc = acc.half().float()
+    return _epilogue(acc, sx, sw, bias), x16, sx, w16, sw
+
+
+def linear_train_bwd(dy2: torch.Tensor, x16: torch.Tensor, sx: torch.Tensor, w: torch.Tensor,
+                     double_round: bool = False):
+    """ScaledLinearFn.backward (autograd.py:71-90) with fp32 accumulation and one
+    bf16 rounding per output; double_round=True also rounds the GEMM result to fp16
+    first, as the reference's cuBLAS fp16 output does (its own error). Returns
+    (dx, dw, db, exps) where exps holds every scale exponent the reference computes."""
+    N, K = w.shape
+    M = dy2.shape[0]
+    rnd = (lambda c: c.half().float()) if double_round else (lambda c: c)
+    dy16, sdy = quantize_rows(dy2, L1_TARGET, l1=True)
+    w16c, swc = quantize_cols(w.contiguous(), target_exp(N))
+    dx = _epilogue(rnd(dy16.float() @ w16c.float()), sdy, swc, None)
+    t = dw_target_exp(M)
+    dy16c, sdyc = quantize_cols(dy2, t, sx)
+    dw = _epilogue(rnd(dy16c.float().t() @ x16.float()), sdyc, torch.ones(K), None)
+    db = dy2.float().sum(0).to(dy2.dtype)
+    exps = {"sdy": sdy, "swc": swc, "sdyc": sdyc}
+    return dx, dw, db, exps
+
+
+# ---------------------------------------------------------------------------
+# a11 - a15: attention
+# ---------------------------------------------------------------------------
+
+def head_amax(x: torch.Tensor) -> torch.Tensor:
+    """small_kernels.cu:222-243: max |x[b, h]| over (S, D), fp32 (B, H)."""
+    if x.shape[2] == 0 or x.shape[3] == 0:
+        return torch.zeros(x.shape[0], x.shape[1])
+    return x.float().abs().amax(dim=(-2, -1))
+
+
+def head_exp(x: torch.Tensor) -> torch.Tensor:
+    """tbf16/attention.py:253-256: frexp exponent of each head's amax, int32."""
+    return torch.frexp(head_amax(x))[1].to(torch.int32)
+
+
+def attn_exponents(q, k, v, v_exp: int):
+    """prepare_qkv exponents (attention.py:267-277): a (scalar) and ev (B, Hkv)."""
+    eq = int(head_exp(q).max())
+    ek = int(head_exp(k).max())
+    a = (ek - eq) // 2
+    a = max(min(a, 14 - eq), ek - 14)
+    ev = head_exp(v) - v_exp
+    return a, ev
+
+
+def head_scale(x: torch.Tensor, e: torch.Tensor, dtype) -> torch.Tensor:
+    """attention.py:259-264: x * 2**e[b, h] cast to dtype (contiguous)."""
+    e = e.to(torch.int32).expand(x.shape[0], x.shape[1])
+    s = torch.ldexp(torch.ones(e.shape), e.float())
+    return (x.float() * s[..., None, None]).to(dtype).contiguous()
+
+
+def expand_heads(e: torch.Tensor, n_heads: int) -> torch.Tensor:
+    """attention.py:280-282."""
+    return e if e.shape[1] == n_heads else e.repeat_interleave(n_heads // e.shape[1], dim=1)
+
+
+def prepare_qkv(q, k, v, v_exp: int = 0):
+    """attention.py:267-277: scaled fp16 copies and the exponents."""
+    a, ev = attn_exponents(q, k, v, v_exp)
+    at = torch.tensor([[a]], dtype=torch.int32)
+    q16 = head_scale(q, at, torch.float16)
+    k16 = head_scale(k, -at, torch.float16)
+    v16 = head_scale(v, -ev, torch.float16)
+    return q16, k16, v16, a, ev
+
+
+def causal_mask(Sq: int, Sk: int) -> torch.Tensor:
+    """is_causal: query i sees keys j <= i (top-left aligned, as torch SDPA)."""
+    return torch.ones(Sq, Sk, dtype=torch.bool).tril(0)
+
+
+def sdpa_ref64(q, k, v, causal=False, scale=None, mask=None, rows=None):
+    """fp64 softmax(q k^T * scale + mask) v of the same bf16 values
+    (tests/test_attention.py:7-13). `rows` restricts the query rows (each row
+    depends only on its own q and all of k, v). GQA by repeating kv heads."""
+    qd, kd, vd = q.double(), k.double(), v.double()
+    H, Hkv = q.shape[1], k.shape[1]
+    if Hkv != H:
+        kd = kd.repeat_interleave(H // Hkv, 1)
+        vd = vd.repeat_interleave(H // Hkv, 1)
+    D = q.shape[-1]
+    sc = (1.0 / math.sqrt(D)) if scale is None else scale
+    Sq, Sk = q.shape[2], k.shape[2]
+    idx = torch.arange(Sq) if rows is None else torch.as_tensor(rows)
+    s = (qd[:, :, idx] @ kd.transpose(-1, -2)) * sc
+    if causal:
+        allowed = causal_mask(Sq, Sk)[idx]
+        s = s.masked_fill(~allowed, float("-inf"))
+    if mask is not None:
+        m = mask[..., idx, :] if mask.shape[-2] == Sq and Sq > 1 else mask
+        s = s.masked_fill(~m, float("-inf")) if m.dtype == torch.bool else s + m.double()
+    return torch.softmax(s, -1) @ vd
+
+
+def sdpa_fp16_emulated(q, k, v, causal=False, scale=None, v_exp=13, rows=None):
+    """This build's attention arithmetic on the CPU: fp16 copies scaled by
+    2^a, 2^-a, 2^-ev (attention.py:267-277), logits and softmax in fp32, P
+    rounded to fp16 for P.V, fp32 accumulation, out = bf16(O / l * 2^ev) with one
+    rounding. The reference itself rounds O to fp16 first (attention.py:292-294)."""
+    q16, k16, v16, a, ev = prepare_qkv(q, k, v, v_exp)
+    H, Hkv = q.shape[1], k.shape[1]
+    k16e = k16.repeat_interleave(H // Hkv, 1) if Hkv != H else k16
+    v16e = v16.repeat_interleave(H // Hkv, 1) if Hkv != H else v16
+    D = q.shape[-1]
+    sc = (1.0 / math.sqrt(D)) if scale is None else scale
+    Sq, Sk = q.shape[2], k.shape[2]
+    idx = torch.arange(Sq) if rows is None else torch.as_tensor(rows)
+    s = (q16[:, :, idx].float() @ k16e.float().transpose(-1, -2)) * sc
+    if causal:
+        s = s.masked_fill(~causal_mask(Sq, Sk)[idx], float("-inf"))
+    m = s.amax(-1, keepdim=True)
+    p = torch.exp(s - m)
+    l = p.sum(-1, keepdim=True)
+    o = (p.half().float() @ v16e.float()) / l
+    evq = expand_heads(ev, H).float()
+    return (o * torch.ldexp(torch.ones_like(evq), evq)[..., None, None]).bfloat16(), a, ev
+
+
+def attn_bwd_exponents(dout: torch.Tensor, ev_q: torch.Tensor, D: int):
+    """autograd.py:175-176: e = max(head_exp(dO) + ev_q), t_do = 12 - ceil(log2 D),
+    G = t_do - e (first attempt)."""
+    e = int((head_exp(dout) + ev_q).max())
+    t_do = attn_do_target(D)
+    return e, t_do, t_do - e
+
+
+def attn_bwd_retry(e: int, t_do: int, overflowed, attempts: int = 6):
+    """autograd.py:177-189: try G = t_do - e; on overflow t_do -= 8; after
+    `attempts` failures raise FloatingPointError. `overflowed(G)` says whether the
+    backward at that G overflowed fp16. Returns the G that was accepted."""
+    for _ in range(attempts):
+        G = t_do - e
+        if not overflowed(G):
+            return G
+        t_do -= 8
+    raise FloatingPointError("tbf16 attention backward overflowed fp16 even after rescaling")
+
+
+def sdpa_grads_ref64(q, k, v, dout, causal=False, scale=None, mask=None):
+    """fp64 autograd of softmax attention on the same bf16 values
+    (tests/test_autograd.py:15-19, 34-42). Returns (o, dq, dk, dv)."""
+    qd, kd, vd = (t.detach().double().requires_grad_() for t in (q, k, v))
+    o = sdpa_ref64(qd, kd, vd, causal, scale, mask)
+    o.backward(dout.double())
+    return o.detach(), qd.grad, kd.grad, vd.grad
+
+
+def rel_err(y, ref) -> float:
+    """Relative Frobenius error ||y - ref|| / ||ref|| (tests/test_accuracy.py:6-7)."""
+    y, ref = y.double(), ref.double()
+    return float((y - ref).norm() / ref.norm())

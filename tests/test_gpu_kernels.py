@@ -1,0 +1,273 @@
+"""GPU parity of the HIP kernels against the CPU oracle (bit-exact exponents and
+payloads) and against fp64 (outputs, with the tolerance the north star states:
+relative Frobenius error <= 2e-3 and no worse than the reference's own error,
+which the oracle emulates)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import workloads as W
+from oracle import tbf16_oracle as O
+from tbf16 import _ext, attention, autograd, ops
+import tbf16
+
+from _ref64 import attn_fwd64, rel
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+# slack on "no worse than the reference's own error": accumulation order differs
+REF_SLACK = 1.02
+
+
+def bf16_from_bits(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(bits.astype(np.uint16).view(np.int16)).view(torch.bfloat16)
+
+
+def f16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def row_exps_gpu(x: torch.Tensor, t: int, l1: bool) -> np.ndarray:
+    M, K = x.shape
+    e = torch.empty(M, dtype=torch.int32, device=x.device)
+    _ext.call("tbf16_row_exps", x.data_ptr(), M, K, x.stride(0), t, int(l1), e.data_ptr(), None, _ext.stream())
+    return e.cpu().numpy()
+
+
+def test_native_library_is_the_one_loaded(dev):
+    assert _ext.available()
+    p = _ext.lib_path()
+    assert p.name == "libtbf16_hip.so" and "turing-bf16_amd" in str(p)
+    assert tbf16.is_supported_gpu()
+
+
+# ---- exponents and payloads, exhaustive over bf16 ---------------------------------
+
+@pytest.mark.parametrize("t", [-1, 0, 15])
+def test_row_exps_every_bf16_amax(dev, t):
+    """Each row holds one bf16 pattern (and zeros): its max is that pattern.
+    All 32,640 finite non-negative patterns plus +inf, both signs."""
+    bits = np.arange(0, 0x7F81, dtype=np.uint32)  # 0 .. +inf
+    x = torch.zeros(2 * len(bits), 8, dtype=torch.bfloat16)
+    x[: len(bits), 3] = bf16_from_bits(bits)
+    x[len(bits):, 5] = bf16_from_bits(bits | 0x8000)
+    xd = x.to(dev)
+    got = row_exps_gpu(xd, t, False)
+    want = O.row_exps(x, t)
+    assert np.array_equal(got, want)
+    # the L1 variant on the same rows (sum of one value = the value)
+    assert np.array_equal(row_exps_gpu(xd, t, True), O.row_exps(x, t, l1=True))
+
+
+@pytest.mark.parametrize("t,l1", [(15, False), (0, False), (15, True), (-1, False)])
+def test_quantize_rows_payload_every_bf16(dev, t, l1):
+    """All 65,536 bf16 patterns as payload, with row maxima spread over 2^0..2^40 so
+    scaled values fall into fp16's subnormal range (RNE there)."""
+    bits = np.arange(0, 1 << 16, dtype=np.uint32)
+    x = bf16_from_bits(bits).reshape(512, 128).clone()
+    x = torch.where(torch.isnan(x), torch.zeros_like(x), x)
+    g = torch.Generator().manual_seed(1)
+    x[:, 0] = torch.ldexp(torch.ones(512), torch.randint(0, 41, (512,), generator=g).float()).bfloat16()
+    y, s = ops.quantize_rows(x.to(dev), t, l1)
+    y_o, s_o = O.quantize_rows(x, t, l1)
+    assert np.array_equal(f16_bits(y), f16_bits(y_o))
+    assert torch.equal(s.cpu(), s_o)
+
+
+def test_quantize_rows_t_and_cols_t_bit_exact(dev):
+    g = torch.Generator().manual_seed(2)
+    x = (torch.randn(203, 264, generator=g) * torch.exp2(torch.randint(-30, 30, (203, 1), generator=g).float()))
+    x = x.bfloat16()
+    xd = x.to(dev)
+    x16T, sx, exps = autograd._quantize_rows_t(xd, 0)
+    y_o, s_o = O.quantize_rows(x, 0)
+    assert x16T.shape == (264, 208)
+    assert np.array_equal(f16_bits(x16T[:, :203].t()), f16_bits(y_o))
+    assert (x16T[:, 203:] == 0).all()
+    assert torch.equal(sx.cpu(), s_o)
+    assert np.array_equal(exps.cpu().numpy(), O.row_exps(x, 0))
+    rm = torch.ldexp(torch.ones(203), torch.randint(-9, 9, (203,), generator=g).float())
+    for t, r in ((0, None), (-2, rm)):
+        yc, sc = tbf16.autograd.quantize_cols(xd, t, None if r is None else r.to(dev))
+        yo, so = O.quantize_cols(x, t, r)
+        assert np.array_equal(f16_bits(yc), f16_bits(yo)) and torch.equal(sc.cpu(), so)
+
+
+# ---- MFMA layout and epilogue: exact small-integer GEMMs -------------------------
+
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3])
+def test_gemm_small_integers_bit_exact(dev, cfg):
+    """Entries in {-1, 0, 1}, K = 200: every partial sum is an integer below 256, so
+    the fp32 accumulation and the bf16 output are exact and the result must equal
+    the integer product bit for bit. Ragged M, N, K exercise every tile edge; pow2
+    scales and an integer bias exercise the epilogue."""
+    g = torch.Generator().manual_seed(3)
+    M, N, K = 300, 264, 200
+    a = torch.randint(-1, 2, (M, K), generator=g)
+    b = torch.randint(-1, 2, (N, K), generator=g)
+    bias = torch.randint(-8, 9, (N,), generator=g)
+    sa = torch.ldexp(torch.ones(M), torch.randint(-3, 4, (M,), generator=g).float())
+    sb = torch.ldexp(torch.ones(N), torch.randint(-3, 4, (N,), generator=g).float())
+    want = ((a @ b.t()).double() * sa.double()[:, None] * sb.double()[None, :] + bias.double()).bfloat16()
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    a16, b16 = a.half().to(dev), b.half().to(dev)
+    sad, sbd, bd = sa.to(dev), sb.to(dev), bias.bfloat16().to(dev)
+    _ext.call("tbf16_gemm_f16", a16.data_ptr(), M, K, K, sad.data_ptr(), b16.data_ptr(), N, K, sbd.data_ptr(),
+              bd.data_ptr(), y.data_ptr(), N, cfg, _ext.stream())
+    assert torch.equal(y.cpu(), want)
+    # bf16 activations through the fused path: row max 1 -> scale 2^14, exact
+    xb = a.bfloat16().to(dev)
+    e = torch.empty(M, dtype=torch.int32, device=dev)
+    ones = torch.ones(N, device=dev)
+    _ext.call("tbf16_linear", xb.data_ptr(), M, K, K, b16.data_ptr(), N, K, ones.data_ptr(), None, y.data_ptr(), N, 15,
+              0, cfg, e.data_ptr(), _ext.stream())
+    assert torch.equal(y.cpu(), (a @ b.t()).bfloat16())
+
+
+def test_gemv_small_integers_bit_exact(dev):
+    g = torch.Generator().manual_seed(4)
+    K, N = 2560, 1000
+    x = torch.randint(-1, 2, (1, K), generator=g).float()
+    x[0, 200:] = 0  # keep |sum| < 256
+    w = torch.randint(-1, 2, (N, K), generator=g).float()
+    ws = torch.ldexp(torch.ones(N), torch.randint(-2, 3, (N,), generator=g).float())
+    y = ops.small_m_linear(x.bfloat16().to(dev), w.half().to(dev), ws.to(dev))
+    assert torch.equal(y.cpu(), ((x @ w.t()) * ws).bfloat16())
+
+
+# ---- Config 1: CPU-path linear (256 x 4096 x 4096, 5 % rows x 2^17) --------------
+
+def _linear_checks(x, w, dev, label):
+    w16, ws = tbf16.prepare_weight(w.to(dev))
+    w16_o, ws_o = O.prepare_weight(w)
+    assert np.array_equal(f16_bits(w16), f16_bits(w16_o)), f"{label}: weight payload"
+    assert torch.equal(ws.cpu(), ws_o), f"{label}: weight exponents"
+    xd = x.to(dev)
+    M = x.shape[0]
+    y = tbf16.scaled_linear(xd, w16, ws)
+    ref = xd.double() @ w.to(dev).double().t()
+    err = rel(y, ref)
+    if M == 1:
+        own = O.gemv(x, w16_o, ws_o)
+    elif M >= O.FUSED_MIN_M:
+        t, l1 = 15, False
+        assert np.array_equal(row_exps_gpu(xd, t, l1), O.row_exps(x, t, l1, fused=True)), f"{label}: x exponents"
+        own = O.linear_fused(x, w16_o, ws_o)
+    else:
+        assert np.array_equal(row_exps_gpu(xd, 15, True), O.row_exps(x, 15, True)), f"{label}: x L1 exponents"
+        own = O.linear_cublas_path(x, w16_o, ws_o)
+    err_own = rel(own.to(dev), ref)
+    print(f"{label}: rel err {err:.3e}  reference's own {err_own:.3e}")
+    assert torch.isfinite(y).all()
+    assert err <= TOL, (label, err)
+    assert err <= err_own * REF_SLACK + 1e-6, (label, err, err_own)
+    return err
+
+
+def test_cfg1_cpu_path_linear(dev):
+    x, w, _ = W.cfg1_cpu_linear()
+    _linear_checks(x, w, dev, "cfg1 256x4096x4096")
+
+
+def test_cfg2_square_gemm(dev):
+    x, w, _ = W.cfg2_square_gemm()
+    _linear_checks(x, w, dev, "cfg2 4096^3")
+
+
+@pytest.mark.parametrize("M", W.CFG3_MS)
+def test_cfg3_small_m(dev, M):
+    w, xs = W.cfg3_small_m()
+    _linear_checks(xs[M], w, dev, f"cfg3 M={M}")
+
+
+# ---- Config 4: scaled attention forward ------------------------------------------
+
+def _attn_checks(q, k, v, dev, rows=None, label=""):
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o, _, _, exps = attention.attn_forward(qd, kd, vd, None, True, None, v_exp=13)
+    a_o, ev_o = O.attn_exponents(q, k, v, 13)
+    ex = exps.cpu()
+    assert int(ex[0]) == a_o, f"{label}: a"
+    assert torch.equal(ex[2:].reshape(ev_o.shape), ev_o.int()), f"{label}: ev"
+    ref = attn_fwd64(qd, kd, vd, True, rows=rows)
+    got = o if rows is None else o[:, :, torch.as_tensor(rows, device=dev)]
+    err = rel(got, ref)
+    # the reference's own result rounds O/l to fp16 before the bf16 scale-back:
+    # apply that double rounding to the exact values (a lower bound on its error)
+    evq = torch.ldexp(torch.ones_like(ev_o, dtype=torch.float64), ev_o.double()).to(dev)[..., None, None]
+    own = ((ref / evq).half().double() * evq).bfloat16()
+    err_own = rel(own, ref)
+    print(f"{label}: rel err {err:.3e}  reference's double rounding alone {err_own:.3e}")
+    assert torch.isfinite(got).all()
+    assert err <= TOL, (label, err)
+    return err, err_own
+
+
+def test_cfg4_attention_4k(dev):
+    q, k, v = W.cfg4_attention(4096)
+    _attn_checks(q, k, v, dev, label="cfg4 S=4096")
+
+
+def test_cfg4_attention_16k_sampled_rows(dev):
+    q, k, v = W.cfg4_attention(16384)
+    g = torch.Generator().manual_seed(5)
+    rows = torch.cat([torch.arange(0, 64), torch.randint(64, 16384, (192,), generator=g), torch.arange(16320, 16384)])
+    _attn_checks(q, k, v, dev, rows=rows.sort().values, label="cfg4 S=16384")
+
+
+# ---- Config 5: training step --------------------------------------------------------
+
+def test_cfg5_linear_fwd_bwd(dev):
+    x, w, dy = W.cfg5_train_linear()
+    M, K = x.shape
+    N = w.shape[0]
+    xd = x.to(dev).requires_grad_()
+    wd = w.to(dev).requires_grad_()
+    y = autograd.linear(xd, wd)
+    y.backward(dy.to(dev))
+    # exponents of every quantisation the reference makes, bit-exact
+    x16T, sx, exps = autograd._quantize_rows_t(x.to(dev), O.target_exp(K))
+    assert np.array_equal(exps.cpu().numpy(), O.row_exps(x, O.target_exp(K)))
+    _, sdy = ops.quantize_rows(dy.to(dev), 15, True)
+    assert torch.equal(sdy.cpu(), O.quantize_rows(dy, 15, True)[1])
+    _, swc = autograd._quantize_cols_t(w.to(dev), O.target_exp(N))
+    assert torch.equal(swc.cpu(), O.quantize_cols(w, O.target_exp(N))[1])
+    sx_o = O.quantize_rows(x, O.target_exp(K))[1]
+    _, sdyc = autograd._quantize_cols_t(dy.to(dev), O.dw_target_exp(M), sx)
+    assert torch.equal(sdyc.cpu(), O.quantize_cols(dy, O.dw_target_exp(M), sx_o)[1])
+    # gradients vs fp64, and vs the reference's own (fp16-output) arithmetic
+    xg, wg, dg = x.to(dev).double(), w.to(dev).double(), dy.to(dev).double()
+    refs = {"y": xg @ wg.t(), "dx": dg @ wg, "dw": dg.t() @ xg}
+    got = {"y": y, "dx": xd.grad, "dw": wd.grad}
+    y_o, x16_o, sx_o2, _, _ = O.linear_train_fwd(x, w, double_round=True)
+    dx_o, dw_o, _, _ = O.linear_train_bwd(dy, x16_o, sx_o2, w, double_round=True)
+    own = {"y": y_o, "dx": dx_o, "dw": dw_o}
+    for n in refs:
+        e, eo = rel(got[n], refs[n]), rel(own[n].to(dev), refs[n])
+        print(f"cfg5 linear {n}: rel err {e:.3e}  reference's own {eo:.3e}")
+        assert torch.isfinite(got[n]).all() and e <= TOL and e <= eo * REF_SLACK + 1e-6, (n, e, eo)
+
+
+def test_cfg5_attention_fwd_bwd(dev):
+    q, k, v, do = W.cfg5_train_attention()
+    from _ref64 import attn_bwd64
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    o = autograd.sdpa(qd, kd, vd, is_causal=True)
+    o.backward(do.to(dev))
+    # exponents: forward a / ev (v_exp = 0), backward e / G
+    a_o, ev_o = O.attn_exponents(q, k, v, 0)
+    e_o, t_do, G_o = O.attn_bwd_exponents(do, O.expand_heads(ev_o, 16), 128)
+    _, _, _, exps = attention.attn_forward(q.to(dev), k.to(dev), v.to(dev), None, True, None, 0, True, True)
+    assert int(exps[0]) == a_o and torch.equal(exps[2:].cpu().reshape(ev_o.shape), ev_o.int())
+    qv, kv, vv = q.to(dev), k.to(dev), v.to(dev)
+    o2, lse, o16, exps2 = attention.attn_forward(qv, kv, vv, None, True, None, 0, True, True)
+    dq, dk, dv, ex_b = autograd.attn_backward(qv, kv, vv, o16, lse, do.to(dev), exps2, None, 128 ** -0.5, True)
+    assert (int(ex_b[0]), int(ex_b[1])) == (e_o, G_o)
+    ro, rdq, rdk, rdv = attn_bwd64(qv, kv, vv, do.to(dev), True)
+    for n, g_, r_ in (("o", o, ro), ("dq", qd.grad, rdq), ("dk", kd.grad, rdk), ("dv", vd.grad, rdv)):
+        e = rel(g_, r_)
+        print(f"cfg5 attention {n}: rel err {e:.3e}")
+        assert torch.isfinite(g_).all() and e <= TOL, (n, e)

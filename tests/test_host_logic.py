@@ -1,0 +1,114 @@
+"""Host-side control flow that needs no GPU: the attention-backward retry policy
+(forced from the host with an injected attempt), routing thresholds, target
+exponents and the conversion entry point's GPU check."""
+import math
+import warnings
+
+import pytest
+import torch
+import torch.nn as nn
+
+import importlib
+
+import tbf16
+from tbf16 import attention, autograd, ops
+
+convert = importlib.import_module("tbf16.convert")  # the package rebinds `tbf16.convert` to the function
+from oracle import tbf16_oracle as O
+
+
+class _Fake:
+    """Stands in for one backward attempt: overflows for the first `n_bad` calls."""
+
+    def __init__(self, n_bad):
+        self.n_bad, self.t_dos = n_bad, []
+
+    def __call__(self, q, k, v, o16, lse, dout, exps, bias, scale, causal, t_do):
+        self.t_dos.append(t_do)
+        bad = len(self.t_dos) <= self.n_bad
+        z = torch.zeros(1)
+        return z, z, z, torch.zeros(2, dtype=torch.int32), torch.tensor([1 if bad else 0], dtype=torch.int32)
+
+
+def _q(D):
+    return torch.zeros(1, 1, 4, D)
+
+
+@pytest.mark.parametrize("D", [64, 112, 128])
+def test_retry_lowers_t_do_by_8(D):
+    f = _Fake(2)
+    autograd.attn_backward(_q(D), None, None, None, None, None, None, None, 1.0, False, check=True, attempt_fn=f)
+    t0 = 12 - math.ceil(math.log2(D))
+    assert f.t_dos == [t0, t0 - 8, t0 - 16]
+    # same sequence as the oracle's restatement of autograd.py:177-189
+    seq = []
+    O.attn_bwd_retry(0, t0, lambda G: seq.append(G) or len(seq) <= 2)
+    assert [t0 - g for g in seq] == [0, 8, 16] and seq[0] - seq[-1] == 16
+
+
+def test_retry_gives_up_after_six():
+    f = _Fake(100)
+    with pytest.raises(FloatingPointError):
+        autograd.attn_backward(_q(128), None, None, None, None, None, None, None, 1.0, False, check=True,
+                               attempt_fn=f)
+    assert len(f.t_dos) == autograd.ATTN_RETRIES == 6
+
+
+def test_check_disabled_runs_once():
+    f = _Fake(100)
+    autograd.attn_backward(_q(128), None, None, None, None, None, None, None, 1.0, False, check=False, attempt_fn=f)
+    assert f.t_dos == [5]
+
+
+def test_target_exp_matches_oracle():
+    for K in (1, 7, 8, 100, 2048, 2560, 4096, 32768, 32769, 65536, 1 << 20):
+        assert ops._target_exp(K) == O.target_exp(K)
+
+
+def test_convert_without_gpu_warns_and_returns_model():
+    m = nn.Sequential(nn.Linear(16, 16))
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        out = tbf16.convert(m)
+    assert out is m and isinstance(m[0], nn.Linear) and type(m[0]) is nn.Linear
+    assert any("MI355X" in str(x.message) for x in w)
+
+
+def test_convert_train_swaps_class_only():
+    m = nn.Sequential(nn.Linear(16, 16), nn.ReLU(), nn.Linear(16, 4))
+    p0 = [id(p) for p in m.parameters()]
+    tbf16.convert(m, train=True, sdpa=False, force=True)
+    assert type(m[0]) is convert.TrainLinear and type(m[2]) is convert.TrainLinear
+    assert [id(p) for p in m.parameters()] == p0
+
+
+def test_mask_to_bias_shapes():
+    keep = torch.ones(2, 7, dtype=torch.bool)
+    keep[:, 5:] = False
+    b = attention.mask_to_bias(keep[:, None, None, :], 2, 3, 4, 7, torch.device("cpu"))
+    assert b.shape == (2, 3, 4, 7) and b.dtype == torch.float16 and b.stride(-1) == 1
+    assert b.stride(1) == 0 and b.stride(2) == 0
+    assert torch.isinf(b[:, :, :, 5:]).all() and (b[:, :, :, :5] == 0).all()
+    add = torch.full((7,), -1e5)
+    b2 = attention.mask_to_bias(add, 2, 3, 4, 7, torch.device("cpu"))
+    assert torch.isinf(b2).all()  # large negatives become -inf in fp16, as the reference
+
+
+def test_router_thresholds():
+    assert convert.MIN_QUERY_ROWS == 16 and ops.FUSED_MIN_M == 256 and ops.SMALL_M == 2 and ops.L1_TARGET == 15
+    # CPU tensors never take the tbf16 path
+    q = torch.randn(1, 2, 32, 64).bfloat16()
+    out = convert._sdpa(q, q, q)
+    assert out.shape == q.shape
+
+
+def test_public_api_names():
+    for n in ["quantize_rows", "scaled_linear", "prepare_weight", "sdpa", "patch", "TuringBF16Mode", "convert",
+              "Linear", "TrainLinear", "autograd", "install_sdpa", "uninstall_sdpa", "is_supported_gpu"]:
+        assert hasattr(tbf16, n)
+    for n in ["linear", "sdpa", "quantize_cols", "ScaledLinearFn", "ScaledSDPAFn", "FP32LinearFn"]:
+        assert hasattr(tbf16.autograd, n)
+    for n in ["_target_exp", "linear_q", "small_m_linear", "quantize_rows_shared"]:
+        assert hasattr(tbf16.ops, n)
+    for n in ["head_exp", "head_scale", "prepare_qkv", "expand_heads"]:
+        assert hasattr(tbf16.attention, n)

@@ -1,0 +1,296 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Each check is chosen so that a plausible slip in the restatement (an off-by-one
+in the exponent offset, a missing clamp, truncation instead of round-to-nearest,
+a transposed operand, a dropped scale) fails: closed-form invariants,
+torch's own RNE casts, an independent C restatement, brute force on tiny inputs
+and fp64 references with closed-form special cases.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pow2_c
+from oracle import tbf16_oracle as O
+
+ALL_BF16 = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+POS_BF16 = np.arange(0, 0x8000, dtype=np.uint32).astype(np.uint16)
+
+
+def bf16_vals(bits):
+    return O.bf16_bits_to_f32(bits)
+
+
+@pytest.mark.parametrize("t", [-1, 0, 1, 5, 15])
+def test_pow2_exp_invariant_on_every_normal_bf16(t):
+    """amax * 2^p lands in [2^(t-1), 2^t) for every normal bf16 amax whose scale
+    is not clamped (small_kernels.cu:11-18 comment)."""
+    a = bf16_vals(POS_BF16)
+    E = O.exp_field(a)
+    p = O.pow2_exp(a, t)
+    ok = (E >= 1) & (E <= 252) & (253 + t - E >= 1) & (253 + t - E <= 254)
+    scaled = a[ok].astype(np.float64) * np.ldexp(1.0, p[ok].astype(np.int64))
+    assert np.all(scaled >= 2.0 ** (t - 1)) and np.all(scaled < 2.0 ** t)
+    # frexp identity for the same values: p = t - frexp_exp(amax)
+    assert np.array_equal(p[ok], t - O.frexp_exp(a[ok]))
+
+
+@pytest.mark.parametrize("t", [-1, 0, 15])
+def test_pow2_exp_c_matches_numpy_all_patterns(t):
+    a = bf16_vals(ALL_BF16)
+    a = np.abs(a)
+    for fused in (False, True):
+        ref = O.pow2_exp_fused(a, t) if fused else O.pow2_exp(a, t)
+        assert np.array_equal(pow2_c.pow2_exp(a, t, fused), ref)
+
+
+def test_pow2_exp_edge_table():
+    """Edge rows written out by hand from the clamps."""
+    f = np.float32
+    # zero row: e clamps to 1 -> se = clamp(252 + t, 1, 254)
+    assert O.pow2_exp(f(0), 15) == 127 and O.pow2_exp(f(0), 0) == 125 and O.pow2_exp(f(0), -1) == 124
+    # fused variant has the same upper clamp
+    assert O.pow2_exp_fused(f(0), 15) == 127
+    # amax = 1.0 (E = 127): s = 2^(t-1)
+    for t in (-1, 0, 15):
+        assert O.pow2_exp(f(1.0), t) == t - 1
+    # huge amax: e clamps to 252 -> se = 1 + t (clamped to >= 1 in the small kernels)
+    assert O.pow2_exp(f(np.inf), 0) == -126 and O.pow2_exp(f(np.inf), 15) == -111
+    assert O.pow2_exp_fused(f(np.inf), -1) == -127   # no lower clamp: se = 0
+    # the Triton variant overflows the scale for zero rows at t = 15 (documented divergence)
+    assert O.pow2_exp_triton(f(0), 15) == 140
+
+
+@pytest.mark.parametrize("p", [-126, -20, -1, 0, 3, 15, 29, 60, 127])
+def test_scaled_f16_matches_torch_rne(p):
+    """fp16(bf16 * 2^p): the C restatement, torch's RNE cast and the oracle agree
+    on all 65,536 bf16 patterns (NaNs compared as NaN)."""
+    x = bf16_vals(ALL_BF16)
+    s = np.float32(np.ldexp(1.0, p))
+    prod = (x * s).astype(np.float32)
+    torch_bits = torch.from_numpy(prod).half().view(torch.int16).numpy().view(np.uint16)
+    c_bits = pow2_c.scaled_f16_bits(ALL_BF16, p)
+    nan_t = np.isnan(torch.from_numpy(torch_bits.view(np.int16)).view(torch.float16).float().numpy())
+    nan_c = (c_bits & 0x7C00) == 0x7C00
+    nan_c &= (c_bits & 0x3FF) != 0
+    assert np.array_equal(nan_t, nan_c)
+    assert np.array_equal(torch_bits[~nan_t], c_bits[~nan_t])
+
+
+def test_f32_to_f16_exhaustive_sample():
+    rng = np.random.default_rng(0)
+    u = rng.integers(0, 1 << 32, size=2_000_000, dtype=np.uint64).astype(np.uint32)
+    x = u.view(np.float32)
+    x = x[np.isfinite(x)]
+    tb = torch.from_numpy(x).half().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(pow2_c.f32_to_f16_bits(x), tb)
+
+
+def test_f32_to_bf16_rne():
+    rng = np.random.default_rng(1)
+    u = rng.integers(0, 1 << 32, size=2_000_000, dtype=np.uint64).astype(np.uint32)
+    x = u.view(np.float32)
+    x = np.concatenate([x[np.isfinite(x)], np.array([0.0, -0.0, np.inf, -np.inf, 1.00390625, 1.01171875], np.float32)])
+    tb = torch.from_numpy(x).bfloat16().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(pow2_c.f32_to_bf16_bits(x), tb)
+    assert np.array_equal(O.f32_to_bf16_rne_bits(x), tb)
+
+
+def _brute_quantize_rows(x, t, l1):
+    """Pure-Python loop restatement of quantize_rows on a tiny input, using
+    math.frexp for the exponent instead of exponent bits."""
+    rows = []
+    sinv = []
+    for r in range(x.shape[0]):
+        vals = [float(v) for v in x[r].float()]
+        amax = sum(abs(v) for v in vals) if l1 else max([abs(v) for v in vals] + [0.0])
+        amax = float(np.float32(amax))
+        if amax == 0.0 or amax < 2.0 ** -126:
+            e = 1 - 127 + 1  # E clamped to 1 -> frexp-style exponent of 2^-126 is -125
+        else:
+            e = math.frexp(amax)[1]
+        p = max(-126, min(127, t - e))
+        rows.append([v * 2.0 ** p for v in vals])
+        sinv.append(2.0 ** -p)
+    y = torch.tensor(rows, dtype=torch.float64).float().half()
+    return y, torch.tensor(sinv, dtype=torch.float32)
+
+
+@pytest.mark.parametrize("l1", [False, True])
+@pytest.mark.parametrize("t", [0, 15])
+def test_quantize_rows_brute_force(l1, t):
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(6, 24, generator=g) * torch.tensor([1e-30, 1e-3, 1, 3e4, 1e20, 0.0])[:, None]
+    x = x.bfloat16()
+    y, s = O.quantize_rows(x, t, l1)
+    yb, sb = _brute_quantize_rows(x, t, l1)
+    assert torch.equal(y.view(torch.int16), yb.view(torch.int16))
+    assert torch.equal(s, sb)
+    # round trip: with the max at 2^14 nothing in these rows is an fp16 subnormal,
+    # so y * s_inv reproduces x exactly
+    if t == 15 and not l1:
+        assert torch.equal((y[1:5].float() * s[1:5, None]).bfloat16(), x[1:5])
+
+
+def test_quantize_cols_matches_rows_of_transpose():
+    g = torch.Generator().manual_seed(4)
+    x = (torch.randn(40, 16, generator=g) * 7).bfloat16()
+    yc, sc = O.quantize_cols(x, 0)
+    yr, sr = O.quantize_rows(x.t().contiguous(), 0)
+    assert torch.equal(yc.t().contiguous().view(torch.int16), yr.view(torch.int16))
+    assert torch.equal(sc, sr)
+    # row_mul: pow2 multipliers folded before the column amax
+    rm = torch.ldexp(torch.ones(40), torch.randint(-5, 6, (40,), generator=g).float())
+    yc2, sc2 = O.quantize_cols(x, -1, rm)
+    xr = (x.float() * rm[:, None]).bfloat16()  # exact: pow2 multiples of bf16 values
+    yr2, sr2 = O.quantize_rows(xr.t().contiguous(), -1)
+    assert torch.equal(yc2.t().contiguous().view(torch.int16), yr2.view(torch.int16)) and torch.equal(sc2, sr2)
+
+
+def test_target_exps():
+    assert [O.target_exp(k) for k in (1, 8, 2048, 2560, 4096, 6144, 32768, 32769, 65536, 1 << 20)] == \
+        [0, 0, 0, 0, 0, 0, 0, -1, -1, -3]
+    # the bound the target is chosen for: K * 4^t <= 65504 (ops.py:41-42)
+    for K in (2048, 32768, 40000, 1 << 20):
+        assert K * 4.0 ** O.target_exp(K) <= 65536
+    assert O.dw_target_exp(8192) == 0 and O.dw_target_exp(40000) == -1 and O.dw_target_exp(1 << 17) == -2
+    assert O.attn_do_target(128) == 5 and O.attn_do_target(64) == 6 and O.attn_do_target(112) == 5
+
+
+def test_linear_paths_vs_fp64():
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(64, 256, generator=g) * 3e4).bfloat16()
+    w = (torch.randn(96, 256, generator=g) * 256 ** -0.5).bfloat16()
+    b = torch.randn(96, generator=g).bfloat16()
+    ref = O.linear_ref64(x, w, b)
+    w16, ws = O.prepare_weight(w)
+    for fn in (O.linear_fused, O.linear_small_m, O.linear_cublas_path):
+        assert O.rel_err(fn(x, w16, ws, b), ref) < 3e-3
+    # single rounding beats the double-rounding cuBLAS path emulation
+    assert O.rel_err(O.linear_small_m(x, w16, ws, b), ref) <= O.rel_err(O.linear_cublas_path(x, w16, ws, b), ref)
+    # GEMV
+    assert O.rel_err(O.gemv(x[:1], w16, ws, b), O.linear_ref64(x[:1], w, b)) < 3e-3
+
+
+def test_linear_exact_small_integers():
+    """Small integers: every product and partial sum is exact in fp32 and the
+    result is exactly representable in bf16, so the emulation must be bit-exact
+    against integer arithmetic. A transposed operand or a dropped scale fails."""
+    g = torch.Generator().manual_seed(6)
+    x = torch.randint(-4, 5, (16, 32), generator=g).float()
+    w = torch.randint(-3, 4, (24, 32), generator=g).float()
+    x[3] = 0  # zero row -> 0 output
+    y_int = (x.long() @ w.long().t()).float()
+    xb, wb = x.bfloat16(), w.bfloat16()
+    w16, ws = O.prepare_weight(wb)
+    for fn in (O.linear_fused, O.linear_small_m):
+        assert torch.equal(fn(xb, w16, ws).float(), y_int)
+    assert torch.equal(O.scaled_linear(xb[:1], w16, ws).float(), y_int[:1])
+    assert torch.equal(O.linear_fused(xb[:, :32], w16, ws)[3].float(), torch.zeros(24))
+
+
+def test_head_exp_and_attn_exponents_brute_force():
+    g = torch.Generator().manual_seed(7)
+    q = (torch.randn(2, 3, 8, 16, generator=g) * torch.tensor([1, 100, 3e-5])[None, :, None, None]).bfloat16()
+    k = (torch.randn(2, 3, 8, 16, generator=g) * 1e4).bfloat16()
+    v = (torch.randn(2, 3, 8, 16, generator=g) * 2.0 ** -9).bfloat16()
+    v[1, 2] = 0
+    he = O.head_exp(q)
+    for b in range(2):
+        for h in range(3):
+            am = max(abs(float(t)) for t in q[b, h].flatten())
+            assert int(he[b, h]) == (math.frexp(am)[1] if am else 0)
+    a, ev = O.attn_exponents(q, k, v, 13)
+    eq = max(math.frexp(max(abs(float(t)) for t in q[b, h].flatten()))[1] for b in range(2) for h in range(3))
+    ek = max(math.frexp(max(abs(float(t)) for t in k[b, h].flatten()))[1] for b in range(2) for h in range(3))
+    a_ref = math.floor((ek - eq) / 2)
+    a_ref = max(min(a_ref, 14 - eq), ek - 14)
+    assert a == a_ref
+    assert int(ev[1, 2]) == -13 and int(ev[0, 0]) == O.head_exp(v)[0, 0] - 13
+    # scaled maxima stay below 2^14 in magnitude class (attention.py:271-272)
+    assert eq + a <= 14 and ek - a <= 14 or (ek - eq) > 28
+
+
+def test_attention_closed_forms():
+    """q = 0: uniform softmax, so row i of a causal output is the mean of V rows
+    0..i. One-hot peaky logits copy one V row."""
+    g = torch.Generator().manual_seed(8)
+    S, D = 32, 16
+    v = torch.randn(1, 2, S, D, generator=g).bfloat16()
+    k = torch.randn(1, 2, S, D, generator=g).bfloat16()
+    q = torch.zeros(1, 2, S, D).bfloat16()
+    o = O.sdpa_ref64(q, k, v, causal=True)
+    prefix = torch.cumsum(v.double(), 2) / torch.arange(1, S + 1, dtype=torch.float64)[:, None]
+    assert torch.allclose(o, prefix, atol=1e-12)
+    o16, _, _ = O.sdpa_fp16_emulated(q, k, v, causal=True)
+    assert O.rel_err(o16, prefix) < 3e-3
+    # one-hot: k = e_j * big, q = e_j -> query attends to the key sharing its one-hot
+    kk = torch.zeros(1, 1, S, D)
+    qq = torch.zeros(1, 1, S, D)
+    for i in range(S):
+        kk[0, 0, i, i % D] = 60.0
+        qq[0, 0, i, i % D] = 60.0
+    kk[0, 0, D:] = 0
+    vv = torch.randn(1, 1, S, D, generator=g)
+    o = O.sdpa_ref64(qq.bfloat16(), kk.bfloat16(), vv.bfloat16(), causal=False)
+    assert torch.allclose(o[0, 0, :D], vv.bfloat16().double()[0, 0, :D], atol=1e-6)
+
+
+def test_attention_emulation_vs_fp64_scaled_heads():
+    g = torch.Generator().manual_seed(9)
+    q = (torch.randn(1, 2, 64, 32, generator=g) * 2.0 ** 9).bfloat16()
+    k = (torch.randn(1, 2, 64, 32, generator=g) * 2.0 ** 8).bfloat16()
+    v = (torch.randn(1, 2, 64, 32, generator=g) * 2.0 ** 11).bfloat16()
+    ref = O.sdpa_ref64(q, k, v, causal=True)
+    out, a, ev = O.sdpa_fp16_emulated(q, k, v, causal=True)
+    assert O.rel_err(out, ref) < 3e-3
+    # unscaled fp16 logits would overflow: the 2^a / 2^-a split is doing work
+    assert not torch.isfinite((q.half() @ k.half().transpose(-1, -2))).all()
+
+
+def test_attn_bwd_exponents_and_retry():
+    do = (torch.randn(1, 2, 8, 128) * 2.0 ** -20).bfloat16()
+    ev_q = torch.tensor([[3, -2]], dtype=torch.int32)
+    e, t_do, G = O.attn_bwd_exponents(do, ev_q, 128)
+    he = O.head_exp(do)
+    assert e == int(max(he[0, 0] + 3, he[0, 1] - 2)) and t_do == 5 and G == 5 - e
+    # overflow on the first two attempts -> G drops by 8 twice
+    calls = []
+    G_acc = O.attn_bwd_retry(e, t_do, lambda g_: calls.append(g_) or len(calls) <= 2)
+    assert calls == [G, G - 8, G - 16] and G_acc == G - 16
+    with pytest.raises(FloatingPointError):
+        O.attn_bwd_retry(e, t_do, lambda g_: True)
+
+
+def test_attention_grads_fp64_against_finite_difference():
+    """The fp64 autograd reference itself: a directional finite difference."""
+    g = torch.Generator().manual_seed(10)
+    q, k, v = (torch.randn(1, 1, 6, 4, generator=g).double() for _ in range(3))
+    do = torch.randn(1, 1, 6, 4, generator=g).double()
+    o, dq, dk, dv = O.sdpa_grads_ref64(q, k, v, do, causal=True)
+    eps = 1e-6
+    for t, gt in ((q, dq), (k, dk), (v, dv)):
+        d = torch.randn(t.shape, generator=g).double()
+        args = [q, k, v]
+        i = [id(q), id(k), id(v)].index(id(t))
+        ap, am = list(args), list(args)
+        ap[i] = t + eps * d
+        am[i] = t - eps * d
+        fd = ((O.sdpa_ref64(*ap, causal=True) - O.sdpa_ref64(*am, causal=True)) * do).sum() / (2 * eps)
+        assert abs(float(fd) - float((gt * d).sum())) < 1e-6
+
+
+def test_linear_train_bwd_vs_fp64():
+    g = torch.Generator().manual_seed(11)
+    M, K, N = 96, 64, 80
+    x = (torch.randn(M, K, generator=g) * 1e4).bfloat16()
+    w = (torch.randn(N, K, generator=g) * K ** -0.5).bfloat16()
+    dy = (torch.randn(M, N, generator=g) * 1e-8).bfloat16()
+    y, x16, sx, w16, sw = O.linear_train_fwd(x, w)
+    dx, dw, db, _ = O.linear_train_bwd(dy, x16, sx, w)
+    assert O.rel_err(y, O.linear_ref64(x, w)) < 3e-3
+    assert O.rel_err(dx, dy.double() @ w.double()) < 3e-3
+    assert O.rel_err(dw, dy.double().t() @ x.double()) < 3e-3
+    assert O.rel_err(db.float(), dy.double().sum(0)) < 3e-3

@@ -1,0 +1,38 @@
+// Host-side helpers shared by the C-ABI entry points: thread-local error text,
+// precondition checks and launch checks.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/tbf16_hip.h"
+
+namespace tbf16 {
+
+void set_error(const char* fmt, ...);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace tbf16
+
+#define TB_CHECK(cond, ...)           \
+  do {                                \
+    if (!(cond)) {                    \
+      ::tbf16::set_error(__VA_ARGS__); \
+      return TBF16_EINVAL;            \
+    }                                 \
+  } while (0)
+
+#define TB_LAUNCH_CHECK(name)                                                                 \
+  do {                                                                                        \
+    hipError_t e_ = hipGetLastError();                                                        \
+    if (e_ != hipSuccess) {                                                                   \
+      ::tbf16::set_error("%s: kernel launch failed: %s", name, hipGetErrorString(e_));       \
+      return TBF16_ELAUNCH;                                                                   \
+    }                                                                                         \
+  } while (0)

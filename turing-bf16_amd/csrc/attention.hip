@@ -1,0 +1,424 @@
+// Scaled attention forward on CDNA4 fp16 MFMA (flash-style, no S x S buffer).
+//
+// Exponents (tbf16/attention.py:267-277), computed in each block's prologue from
+// per-head partial maxima written by a memory-bound pre-pass:
+//   eq = max_{b,h} frexp(amax q[b,h]), ek likewise, a = floor((ek - eq) / 2)
+//   clamped to [ek - 14, 14 - eq], ev[b, hkv] = frexp(amax v[b, hkv]) - v_exp.
+// q, k, v are read as bf16 and converted on the fly: q16 = q * 2^a, k16 = k * 2^-a,
+// v16 = v * 2^-ev (exact powers of two), so no scaled copies exist in HBM.
+//
+// Block = 4 waves, 128 query rows (32 per wave); key tiles of 64.
+//  - a wave keeps its 32 q rows as MFMA fragments in registers for the whole
+//    kernel and computes S^T = K Q^T with v_mfma_f32_32x32x16_f16 (K from LDS), so
+//    each lane owns ONE query row: row max / sum need one exchange with lane ^ 32.
+//  - online softmax in fp32, base 2 (logit * scale * log2 e), P rounded to fp16.
+//  - O^T = V^T P^T: V is stored transposed in LDS (d-major, keys permuted within
+//    each 16-key group by swapping index bits 2 and 3) so that the A fragment of
+//    a lane is one 16-byte read and P's fragment comes straight from S^T's
+//    accumulators without any cross-lane shuffle.
+//  - output bf16(O / l * 2^ev) written from registers: one rounding.
+// Causal blocks are launched heaviest first; key tiles past the diagonal are
+// skipped, only tiles crossing it are masked.
+#include <algorithm>
+#include <math.h>
+
+#include "abi_util.h"
+#include "common.h"
+
+using namespace tbf16;
+
+namespace tbf16 {
+int64_t head_amax_chunks(int64_t BH, int64_t S);
+int launch_head_amax_partial(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                             int64_t sh, int64_t ss, float* partial, int64_t nchunks, hipStream_t st);
+}  // namespace tbf16
+
+namespace {
+
+constexpr int BQ = 128, BKV = 64, NTH = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct FwdParams {
+  const uint16_t *q, *k, *v;
+  int64_t q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss;
+  const uint16_t* bias;
+  int64_t bias_sb, bias_sh, bias_sq;
+  int B, H, Hkv, Sq, Sk, D;
+  float scale_log2;
+  int v_exp;
+  const float *part_q, *part_k, *part_v;
+  int nch_q, nch_k, nch_v;
+  uint16_t* o;
+  float* lse;
+  uint16_t* o16;
+  int32_t* exps;
+};
+
+__device__ __forceinline__ int perm16(int key) {  // swap bits 2 and 3 of a key index
+  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+
+template <int DP>
+__device__ __forceinline__ int swz_k(int row, int chunk) {
+  constexpr int RB = DP * 2;
+  if constexpr (DP >= 128) return row * RB + ((chunk ^ (row & 15)) << 4);
+  else return row * RB + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+
+__device__ __forceinline__ int swz_vt(int d, int chunk) { return d * 128 + ((chunk ^ ((d >> 1) & 7)) << 4); }
+
+// Block-wide max of an int (256 threads).
+__device__ __forceinline__ int block_max_int(int v, int* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+// max over heads of frexp(max over chunks of partial[bh][c])
+__device__ int heads_max_exp(const float* part, int nbh, int nch, int* red) {
+  int e = INT_MIN;
+  for (int bh = threadIdx.x; bh < nbh; bh += NTH) {
+    float m = 0.f;
+    for (int c = 0; c < nch; ++c) m = fmaxf(m, part[bh * nch + c]);
+    e = max(e, frexp_exp(m));
+  }
+  return block_max_int(e, red);
+}
+
+__device__ __forceinline__ int head_exp_of(const float* part, int bh, int nch) {
+  float m = 0.f;
+  for (int c = 0; c < nch; ++c) m = fmaxf(m, part[bh * nch + c]);
+  return frexp_exp(m);
+}
+
+template <int DP, bool CAUSAL, bool HAS_BIAS>
+__global__ __launch_bounds__(NTH) void attn_fwd_kernel(FwdParams p) {
+  constexpr int KS = DP / 16;            // MFMA k-steps over the head dim
+  constexpr int DB = DP / 32;            // 32-wide d blocks of O^T
+  constexpr int CPR = DP / 8;            // 16-byte chunks per K row
+  constexpr int KROWS = NTH / CPR;       // K rows per load pass
+  constexpr int KL = BKV / KROWS;        // K loads per thread
+  constexpr int VBLK = 16 * (DP / 8);    // 4-key x 8-d blocks in a V tile
+  constexpr int VL = (VBLK + NTH - 1) / NTH;
+  constexpr int KBYTES = BKV * DP * 2;
+  constexpr int STAGE = KBYTES + DP * 128;
+  __shared__ __align__(16) uint8_t smem[2 * STAGE];
+  __shared__ int red[4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, fk = lane >> 5;
+  const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
+  const int hk = h / (p.H / p.Hkv);
+  const int qt = CAUSAL ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;
+  const int q0 = qt * BQ;
+
+  // ---- exponents ----
+  const int eq = heads_max_exp(p.part_q, p.B * p.H, p.nch_q, red);
+  const int ek = heads_max_exp(p.part_k, p.B * p.Hkv, p.nch_k, red);
+  int a = (ek - eq) >> 1;  // floor division
+  a = max(min(a, 14 - eq), ek - 14);
+  const int ev = head_exp_of(p.part_v, b * p.Hkv + hk, p.nch_v) - p.v_exp;
+  if (p.exps && blockIdx.x == 0 && blockIdx.y == 0) {
+    if (tid == 0) {
+      p.exps[0] = a;
+      p.exps[1] = 0;
+    }
+    for (int i = tid; i < p.B * p.Hkv; i += NTH) p.exps[2 + i] = head_exp_of(p.part_v, i, p.nch_v) - p.v_exp;
+  }
+  const float sq = ldexp1(a), sk = ldexp1(-a), sv = ldexp1(-ev);
+
+  // ---- Q fragments in registers (fp16, scaled by 2^a) ----
+  const int qrow = q0 + wave * 32 + fr;
+  half8 qf[KS];
+  {
+    const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)min(qrow, p.Sq - 1) * p.q_ss;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int d = 16 * s + 8 * fk;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (qrow < p.Sq && d < p.D) v = cvt_bf16x8_f16x8(ldg16(qp + d), sq);
+      qf[s] = __builtin_bit_cast(half8, v);
+    }
+  }
+
+  // ---- K / V staging ----
+  const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const uint16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
+  uint4 rk[KL];
+  uint4 rv[VL][4];
+  auto gload = [&](int kb) {
+    const int key0 = kb * BKV;
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      const int row = tid / CPR + i * KROWS, c = tid % CPR;
+      const int key = key0 + row, d = c * 8;
+      rk[i] = (key < p.Sk && d < p.D) ? ldg16(kbase + (int64_t)key * p.k_ss + d) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      const int blk = tid + i * NTH;
+      const int kg = blk & 15, dc = blk >> 4;
+      const int d = dc * 8;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = key0 + 4 * kg + r;
+        rv[i][r] = (blk < VBLK && key < p.Sk && d < p.D) ? ldg16(vbase + (int64_t)key * p.v_ss + d)
+                                                        : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto lstore = [&](int stg) {
+    uint8_t* sK = smem + stg * STAGE;
+    uint8_t* sV = sK + KBYTES;
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      const int row = tid / CPR + i * KROWS, c = tid % CPR;
+      *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, c)) = cvt_bf16x8_f16x8(rk[i], sk);
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      const int blk = tid + i * NTH;
+      if (blk >= VBLK) continue;
+      const int kg = blk & 15, dc = blk >> 4;
+      uint4 cv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) cv[r] = cvt_bf16x8_f16x8(rv[i][r], sv);
+      const int pos = perm16(4 * kg);  // 4 consecutive keys stay consecutive
+      const int chunk = pos >> 3, half_off = (pos & 7) * 2;
+      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
+      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
+      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&cv[2]);
+      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int sh = (j & 1) * 16;
+        const uint32_t e0 = (w0[j >> 1] >> sh) & 0xffffu, e1 = (w1[j >> 1] >> sh) & 0xffffu;
+        const uint32_t e2 = (w2[j >> 1] >> sh) & 0xffffu, e3 = (w3[j >> 1] >> sh) & 0xffffu;
+        const int d = dc * 8 + j;
+        *reinterpret_cast<uint2*>(sV + swz_vt(d, chunk) + half_off) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+      }
+    }
+  };
+
+  floatx16 acc_o[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_o[i][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int nkb_all = (p.Sk + BKV - 1) / BKV;
+  int nkb = nkb_all;
+  if constexpr (CAUSAL) nkb = min(nkb_all, (min(q0 + BQ, p.Sq) + BKV - 1) / BKV);
+  const uint16_t* brow = nullptr;
+  if constexpr (HAS_BIAS)
+    brow = p.bias + (int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh + (int64_t)min(qrow, p.Sq - 1) * p.bias_sq;
+
+  if (nkb > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int stg = kb & 1;
+    if (kb + 1 < nkb) gload(kb + 1);
+    const uint8_t* sK = smem + stg * STAGE;
+    const uint8_t* sV = sK + KBYTES;
+
+    // S^T = K Q^T for two 32-key halves
+    floatx16 sacc[2];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[kh][r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const half8 kf = *reinterpret_cast<const half8*>(sK + swz_k<DP>(kh * 32 + fr, 2 * s + fk));
+        sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[kh], 0, 0, 0);
+      }
+    }
+
+    // logits in log2 units, masking, running max
+    const int key0 = kb * BKV;
+    const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+        float s = sacc[kh][r] * p.scale_log2;
+        if constexpr (HAS_BIAS) {
+          if (key < p.Sk) s += (float)__builtin_bit_cast(_Float16, brow[key]) * kLog2e;
+        }
+        if (edge && (key >= p.Sk || (CAUSAL && key > qrow))) s = -INFINITY;
+        sacc[kh][r] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float lsum = 0.f;
+    uint32_t pk[2][8];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(sacc[kh][r] - m_use);
+        const float p1 = __builtin_amdgcn_exp2f(sacc[kh][r + 1] - m_use);
+        lsum += p0 + p1;
+        pk[kh][r >> 1] = pack_f16(p0, p1);
+      }
+    l_run = l_run * alpha + lsum;
+#pragma unroll
+    for (int i = 0; i < DB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
+
+    // O^T += V^T P^T over four 16-key steps
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const uint4 pw = make_uint4(pk[ks >> 1][4 * (ks & 1) + 0], pk[ks >> 1][4 * (ks & 1) + 1],
+                                  pk[ks >> 1][4 * (ks & 1) + 2], pk[ks >> 1][4 * (ks & 1) + 3]);
+      const half8 pf = __builtin_bit_cast(half8, pw);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const half8 vf = *reinterpret_cast<const half8*>(sV + swz_vt(db * 32 + fr, 2 * ks + fk));
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc_o[db], 0, 0, 0);
+      }
+    }
+
+    if (kb + 1 < nkb) lstore(stg ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (qrow >= p.Sq) return;
+  const float sev = ldexp1(ev);
+  const int64_t orow = ((int64_t)bh * p.Sq + qrow) * p.D;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int d = db * 32 + 8 * rq + 4 * fk;
+      if (d >= p.D) continue;
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = l_tot > 0.f ? acc_o[db][4 * rq + e] / l_tot : 0.f;
+      *reinterpret_cast<uint2*>(p.o + orow + d) =
+          make_uint2(pack_bf16(y[0] * sev, y[1] * sev), pack_bf16(y[2] * sev, y[3] * sev));
+      if (p.o16) *reinterpret_cast<uint2*>(p.o16 + orow + d) = make_uint2(pack_f16(y[0], y[1]), pack_f16(y[2], y[3]));
+    }
+  if (p.lse && fk == 0)
+    // log2(l) via v_log_f32; rows that see no key get +inf so the backward's
+    // exp2(logit - lse) is 0 there
+    p.lse[(int64_t)bh * p.Sq + qrow] = (l_tot > 0.f) ? m_run + __builtin_amdgcn_logf(l_tot) : INFINITY;
+}
+
+struct WsLayout {
+  int64_t nch_q, nch_k, nch_v;
+  size_t off_k, off_v, total;
+};
+
+WsLayout fwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk) {
+  WsLayout w;
+  w.nch_q = head_amax_chunks(B * H, Sq);
+  w.nch_k = head_amax_chunks(B * Hkv, Sk);
+  w.nch_v = w.nch_k;
+  const size_t bq = align_up((size_t)(B * H * w.nch_q) * 4, 256), bk = align_up((size_t)(B * Hkv * w.nch_k) * 4, 256);
+  w.off_k = bq;
+  w.off_v = bq + bk;
+  w.total = bq + 2 * bk;
+  return w;
+}
+
+template <int DP>
+int launch_fwd_dp(const FwdParams& p, bool causal, bool has_bias, dim3 grid, hipStream_t st) {
+  if (causal) {
+    if (has_bias) attn_fwd_kernel<DP, true, true><<<grid, NTH, 0, st>>>(p);
+    else attn_fwd_kernel<DP, true, false><<<grid, NTH, 0, st>>>(p);
+  } else {
+    if (has_bias) attn_fwd_kernel<DP, false, true><<<grid, NTH, 0, st>>>(p);
+    else attn_fwd_kernel<DP, false, false><<<grid, NTH, 0, st>>>(p);
+  }
+  TB_LAUNCH_CHECK("attn_fwd");
+  return 0;
+}
+
+int check_bhsd(const char* fn, const char* name, const void* x, const int64_t* st, int64_t D) {
+  TB_CHECK(x != nullptr && st != nullptr, "%s: %s missing", fn, name);
+  TB_CHECK(aligned16(x) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0,
+           "%s: %s must be (B, H, S, D) with contiguous D %% 8 == 0, 16-byte aligned", fn, name);
+  (void)D;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" size_t tbf16_attn_fwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
+  (void)D;
+  return fwd_ws(B, H, Hkv, Sq, Sk).total;
+}
+
+extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t Hkv,
+                              int64_t Sq, int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
+                              const int64_t* v_strides, const void* bias, const int64_t* bias_strides, float scale,
+                              int causal, int v_exp, void* o, float* lse, void* o16, int32_t* exps, void* ws,
+                              int64_t ws_bytes, void* stream) {
+  TB_CHECK(B >= 0 && H > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0, "attn_fwd: bad shape");
+  TB_CHECK(H % Hkv == 0, "attn_fwd: query heads must be a multiple of key/value heads");
+  TB_CHECK(D > 0 && D % 8 == 0 && D <= 256, "attn_fwd: head dim must be a multiple of 8 up to 256");
+  TB_CHECK(B * H < (int64_t)1 << 31 && Sq < (int64_t)1 << 31 && Sk < (int64_t)1 << 31, "attn_fwd: too large");
+  if (int rc = check_bhsd("attn_fwd", "q", q, q_strides, D)) return rc;
+  if (int rc = check_bhsd("attn_fwd", "k", k, k_strides, D)) return rc;
+  if (int rc = check_bhsd("attn_fwd", "v", v, v_strides, D)) return rc;
+  TB_CHECK(o != nullptr && aligned16(o) && (o16 == nullptr || aligned16(o16)), "attn_fwd: bad output");
+  if (bias) TB_CHECK(bias_strides != nullptr, "attn_fwd: bias strides missing");
+  const WsLayout w = fwd_ws(B, H, Hkv, Sq, Sk);
+  TB_CHECK(ws != nullptr && ws_bytes >= (int64_t)w.total, "attn_fwd: workspace too small");
+  if (B == 0 || Sq == 0) return 0;
+  TB_CHECK(Sk > 0, "attn_fwd: empty key sequence");
+  hipStream_t st = as_stream(stream);
+  float* pq = reinterpret_cast<float*>(ws);
+  float* pk = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_k);
+  float* pv = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_v);
+  if (int rc = launch_head_amax_partial(q, TBF16_DT_BF16, B, H, Sq, D, q_strides[0], q_strides[1], q_strides[2], pq,
+                                        w.nch_q, st))
+    return rc;
+  if (int rc = launch_head_amax_partial(k, TBF16_DT_BF16, B, Hkv, Sk, D, k_strides[0], k_strides[1], k_strides[2],
+                                        pk, w.nch_k, st))
+    return rc;
+  if (int rc = launch_head_amax_partial(v, TBF16_DT_BF16, B, Hkv, Sk, D, v_strides[0], v_strides[1], v_strides[2],
+                                        pv, w.nch_v, st))
+    return rc;
+  FwdParams p;
+  p.q = (const uint16_t*)q;
+  p.k = (const uint16_t*)k;
+  p.v = (const uint16_t*)v;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.bias = (const uint16_t*)bias;
+  p.bias_sb = bias ? bias_strides[0] : 0;
+  p.bias_sh = bias ? bias_strides[1] : 0;
+  p.bias_sq = bias ? bias_strides[2] : 0;
+  p.B = (int)B; p.H = (int)H; p.Hkv = (int)Hkv; p.Sq = (int)Sq; p.Sk = (int)Sk; p.D = (int)D;
+  p.scale_log2 = scale * kLog2e;
+  p.v_exp = v_exp;
+  p.part_q = pq; p.part_k = pk; p.part_v = pv;
+  p.nch_q = (int)w.nch_q; p.nch_k = (int)w.nch_k; p.nch_v = (int)w.nch_v;
+  p.o = (uint16_t*)o;
+  p.lse = lse;
+  p.o16 = (uint16_t*)o16;
+  p.exps = exps;
+  dim3 grid((unsigned)cdiv(Sq, BQ), (unsigned)(B * H));
+  if (D <= 64) return launch_fwd_dp<64>(p, causal != 0, bias != nullptr, grid, st);
+  if (D <= 128) return launch_fwd_dp<128>(p, causal != 0, bias != nullptr, grid, st);
+  return launch_fwd_dp<256>(p, causal != 0, bias != nullptr, grid, st);
+}

@@ -1,0 +1,574 @@
+// Scaled attention backward on CDNA4 fp16 MFMA (flash-style, deterministic).
+//
+// Scaling (tbf16/autograd.py:166-193): e = max_{b,h}(frexp(amax dO[b,h]) + ev_q[b,h]),
+// G = t_do - e, dO16 = fp16(dO * 2^(ev_q + G)); with q16 = q 2^a, k16 = k 2^-a,
+// v16 = v 2^-ev converted on the fly from the bf16 inputs:
+//   P = exp2(S * scale * log2e - lse), dP = dO16 V16^T, delta = rowsum(dO16 * O16),
+//   dS = P (dP - delta),
+//   dv = bf16(sum_q P^T dO16 * 2^(-ev-G)), dk = bf16(scale * sum_q dS^T Q16 * 2^(-a-G)),
+//   dq = bf16(scale * sum_k dS K16 * 2^(a-G)), each from fp32 accumulators.
+// The fp16 values the reference's kernel would round its gradients to are
+// scale * dS K16 (dq16), scale * dS^T Q16 (dk16) and P^T dO16 (dv16): if any of them
+// reaches 65520 or is not finite the overflow flag is raised and the caller retries
+// with t_do - 8 (the reference's condition, tbf16/autograd.py:184-187).
+//
+// Kernels (4 waves, v_mfma_f32_32x32x16_f16):
+//   delta:   one 16-lane group per query row; also computes e, G.
+//   dkdv:    block = 128 keys (32 per wave, K16 / V16 fragments in registers), loops
+//            over 64-query tiles (and over the query heads of a GQA group). Q and
+//            dO tiles sit in LDS twice: row-major (A operand of S = Q K^T and
+//            dP = dO V^T, whose accumulators give each lane ONE key and 16 queries)
+//            and transposed with queries permuted in 16-groups (B operand of
+//            dV += P^T dO and dK += dS^T Q), so P / dS feed the next MFMA
+//            straight from registers.
+//   dq:      block = 128 queries (32 per wave, Q16 / dO16 in registers), loops over
+//            64-key tiles: K row-major + transposed and V row-major in LDS; S^T and
+//            dP^T give each lane ONE query, so dS is the A operand of dQ += dS K.
+#include <algorithm>
+#include <math.h>
+
+#include "abi_util.h"
+#include "common.h"
+
+using namespace tbf16;
+
+namespace tbf16 {
+int64_t head_amax_chunks(int64_t BH, int64_t S);
+int launch_head_amax_partial(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                             int64_t sh, int64_t ss, float* partial, int64_t nchunks, hipStream_t st);
+}  // namespace tbf16
+
+namespace {
+
+constexpr int NTH = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kF16Overflow = 65520.f;
+
+struct BwdParams {
+  const uint16_t *q, *k, *v, *o16, *dout;
+  const float* lse;
+  const int32_t* exps_fwd;  // {a, 0, ev[b*Hkv + hk]...}
+  int64_t q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss, d_sb, d_sh, d_ss;
+  const uint16_t* bias;
+  int64_t bias_sb, bias_sh, bias_sq;
+  int B, H, Hkv, Sq, Sk, D;
+  float scale, scale_log2;
+  int causal;
+  int t_do;
+  const float* part_do;
+  int nch_do;
+  float* delta;     // (B, H, Sq)
+  int32_t* exps_out;  // {e, G}
+  int32_t* overflow;
+  uint16_t *dq, *dk, *dv;
+};
+
+__device__ __forceinline__ int perm16(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+template <int DP>
+__device__ __forceinline__ int swz_row(int row, int chunk) {
+  if constexpr (DP >= 128) return row * (DP * 2) + ((chunk ^ (row & 15)) << 4);
+  else return row * (DP * 2) + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+__device__ __forceinline__ int swz_t(int d, int chunk) { return d * 128 + ((chunk ^ ((d >> 1) & 7)) << 4); }
+
+__device__ __forceinline__ int ev_of(const BwdParams& p, int b, int h) {
+  return p.exps_fwd[2 + b * p.Hkv + h / (p.H / p.Hkv)];
+}
+
+// e = max over (b, h) of frexp(amax dO[b,h]) + ev_q[b,h]  (block-wide)
+__device__ int compute_e(const BwdParams& p, int* red) {
+  int e = INT_MIN;
+  for (int bh = threadIdx.x; bh < p.B * p.H; bh += NTH) {
+    float m = 0.f;
+    for (int c = 0; c < p.nch_do; ++c) m = fmaxf(m, p.part_do[bh * p.nch_do + c]);
+    e = max(e, frexp_exp(m) + ev_of(p, bh / p.H, bh % p.H));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) e = max(e, __shfl_xor(e, o, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = e;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+__device__ __forceinline__ bool bad16(float x) { return !(fabsf(x) < kF16Overflow); }
+
+// ---- delta = rowsum(dO16 * O16), and {e, G} -----------------------------------
+__global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
+  __shared__ int red[4];
+  const int e = compute_e(p, red);
+  const int G = p.t_do - e;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+    p.exps_out[0] = e;
+    p.exps_out[1] = G;
+  }
+  const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
+  const float sdo = ldexp1(ev_of(p, b, h) + G);
+  const int row = blockIdx.x * 16 + (threadIdx.x >> 4), l16 = threadIdx.x & 15;
+  float acc = 0.f;
+  if (row < p.Sq) {
+    const uint16_t* dr = p.dout + (int64_t)b * p.d_sb + (int64_t)h * p.d_sh + (int64_t)row * p.d_ss;
+    const uint16_t* orow = p.o16 + ((int64_t)bh * p.Sq + row) * p.D;
+    for (int d = l16 * 8; d < p.D; d += 128) {
+      const uint4 dv = cvt_bf16x8_f16x8(ldg16(dr + d), sdo);
+      const uint4 ov = ldg16(orow + d);
+      acc += f16_lo(dv.x) * f16_lo(ov.x) + f16_hi(dv.x) * f16_hi(ov.x) + f16_lo(dv.y) * f16_lo(ov.y) +
+             f16_hi(dv.y) * f16_hi(ov.y) + f16_lo(dv.z) * f16_lo(ov.z) + f16_hi(dv.z) * f16_hi(ov.z) +
+             f16_lo(dv.w) * f16_lo(ov.w) + f16_hi(dv.w) * f16_hi(ov.w);
+    }
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (row < p.Sq && l16 == 0) p.delta[(int64_t)bh * p.Sq + row] = acc;
+}
+
+// Loads a 4-row x 8-column bf16 block (rows r0..r0+3 of a strided matrix) as raw uint4s.
+__device__ __forceinline__ void load_blk(const uint16_t* base, int64_t rs, int r0, int rows, int d, int D, uint4 (&v)[4]) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    v[r] = (r0 + r < rows && d < D) ? ldg16(base + (int64_t)(r0 + r) * rs + d) : make_uint4(0, 0, 0, 0);
+}
+
+// Converts a block with scale s and writes it row-major (rows r0l..r0l+3, chunk dc) and
+// transposed (d-major rows dc*8..dc*8+7, columns perm16(r0l..r0l+3)) into LDS.
+template <int DP>
+__device__ __forceinline__ void store_blk_both(uint8_t* sRow, uint8_t* sT, const uint4 (&raw)[4], float s, int r0l,
+                                               int dc) {
+  uint4 cv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    cv[r] = cvt_bf16x8_f16x8(raw[r], s);
+    *reinterpret_cast<uint4*>(sRow + swz_row<DP>(r0l + r, dc)) = cv[r];
+  }
+  const int pos = perm16(r0l);
+  const int chunk = pos >> 3, hoff = (pos & 7) * 2;
+  const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
+  const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
+  const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&cv[2]);
+  const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int sh = (j & 1) * 16;
+    const uint32_t e0 = (w0[j >> 1] >> sh) & 0xffffu, e1 = (w1[j >> 1] >> sh) & 0xffffu;
+    const uint32_t e2 = (w2[j >> 1] >> sh) & 0xffffu, e3 = (w3[j >> 1] >> sh) & 0xffffu;
+    *reinterpret_cast<uint2*>(sT + swz_t(dc * 8 + j, chunk) + hoff) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+  }
+}
+
+// ---- dK, dV --------------------------------------------------------------------
+template <int DP, bool CAUSAL, bool HAS_BIAS>
+__global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
+  constexpr int BQ = 64, BK = 128;
+  constexpr int KS = DP / 16, DB = DP / 32;
+  constexpr int TILE = BQ * DP * 2;                 // one 64 x DP fp16 tile
+  constexpr int NBLK = (BQ / 4) * (DP / 8);         // 4 x 8 blocks per tile
+  constexpr int BL = (NBLK + NTH - 1) / NTH;
+  __shared__ __align__(16) uint8_t smem[4 * TILE];  // Q, Q^T, dO, dO^T
+  __shared__ float s_lse[BQ], s_delta[BQ];
+  uint8_t* sQ = smem;
+  uint8_t* sQT = smem + TILE;
+  uint8_t* sD = smem + 2 * TILE;
+  uint8_t* sDT = smem + 3 * TILE;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, fr = lane & 31, fk = lane >> 5;
+  const int bk = blockIdx.y, b = bk / p.Hkv, hk = bk % p.Hkv;
+  const int k0 = blockIdx.x * BK;
+  const int a = p.exps_fwd[0];
+  const int ev = p.exps_fwd[2 + bk];
+  const int G = p.exps_out[1];
+
+  // wave's 32 keys as fragments (B operand of S = Q K^T and dP = dO V^T)
+  const int key = k0 + wave * 32 + fr;
+  half8 kf[KS], vf[KS];
+  {
+    const float sk = ldexp1(-a), sv = ldexp1(-ev);
+    const uint16_t* kr = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)min(key, p.Sk - 1) * p.k_ss;
+    const uint16_t* vr = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh + (int64_t)min(key, p.Sk - 1) * p.v_ss;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int d = 16 * s + 8 * fk;
+      const bool ok = key < p.Sk && d < p.D;
+      kf[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(kr + d), sk) : make_uint4(0, 0, 0, 0));
+      vf[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(vr + d), sv) : make_uint4(0, 0, 0, 0));
+    }
+  }
+  floatx16 dk[DB], dv[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[i][r] = dv[i][r] = 0.f;
+
+  const int group = p.H / p.Hkv;
+  const int nqt = (p.Sq + BQ - 1) / BQ;
+  const int qt0 = CAUSAL ? min(k0 / BQ, nqt) : 0;
+  const int total = group * (nqt - qt0);
+
+  uint4 rq[BL][4], rd[BL][4];
+  auto gload = [&](int it) {
+    const int h = hk * group + it / (nqt - qt0);
+    const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
+    const uint16_t* qb = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+    const uint16_t* db = p.dout + (int64_t)b * p.d_sb + (int64_t)h * p.d_sh;
+#pragma unroll
+    for (int i = 0; i < BL; ++i) {
+      const int blk = tid + i * NTH;
+      const int kg = blk & 15, dc = blk >> 4;
+      if (blk < NBLK) {
+        load_blk(qb, p.q_ss, q0 + 4 * kg, p.Sq, dc * 8, p.D, rq[i]);
+        load_blk(db, p.d_ss, q0 + 4 * kg, p.Sq, dc * 8, p.D, rd[i]);
+      }
+    }
+  };
+
+  if (total > 0) gload(0);
+  for (int it = 0; it < total; ++it) {
+    const int h = hk * group + it / (nqt - qt0);
+    const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
+    const int bh = b * p.H + h;
+    const float sq = ldexp1(a), sdo = ldexp1(ev + G);
+    __syncthreads();  // previous tile's readers are done
+#pragma unroll
+    for (int i = 0; i < BL; ++i) {
+      const int blk = tid + i * NTH;
+      const int kg = blk & 15, dc = blk >> 4;
+      if (blk < NBLK) {
+        store_blk_both<DP>(sQ, sQT, rq[i], sq, 4 * kg, dc);
+        store_blk_both<DP>(sD, sDT, rd[i], sdo, 4 * kg, dc);
+      }
+    }
+    if (tid < BQ) {
+      const int qi = q0 + tid;
+      s_lse[tid] = qi < p.Sq ? p.lse[(int64_t)bh * p.Sq + qi] : INFINITY;
+      s_delta[tid] = qi < p.Sq ? p.delta[(int64_t)bh * p.Sq + qi] : 0.f;
+    }
+    __syncthreads();
+    if (it + 1 < total) gload(it + 1);
+
+    // S and dP for two 32-query blocks: lane = one key, 16 queries each
+    floatx16 sacc[2], pacc[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[qb][r] = pacc[qb][r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const half8 qa = *reinterpret_cast<const half8*>(sQ + swz_row<DP>(qb * 32 + fr, 2 * s + fk));
+        const half8 da = *reinterpret_cast<const half8*>(sD + swz_row<DP>(qb * 32 + fr, 2 * s + fk));
+        sacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kf[s], sacc[qb], 0, 0, 0);
+        pacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, vf[s], pacc[qb], 0, 0, 0);
+      }
+    }
+    // P and dS (fp16, packed in MFMA k-slot order)
+    uint32_t pp[2][8], ds[2][8];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float pv[2], dsv[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int ql = qb * 32 + 8 * ((r + u) >> 2) + 4 * fk + ((r + u) & 3);
+          const int qi = q0 + ql;
+          float s = sacc[qb][r + u] * p.scale_log2;
+          if constexpr (HAS_BIAS) {
+            if (qi < p.Sq && key < p.Sk)
+              s += (float)__builtin_bit_cast(_Float16, p.bias[(int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh +
+                                                              (int64_t)qi * p.bias_sq + key]) * kLog2e;
+          }
+          float pr = __builtin_amdgcn_exp2f(s - s_lse[ql]);
+          if (key >= p.Sk || qi >= p.Sq || (CAUSAL && key > qi)) pr = 0.f;
+          pv[u] = pr;
+          dsv[u] = pr * (pacc[qb][r + u] - s_delta[ql]);
+        }
+        pp[qb][r >> 1] = pack_f16(pv[0], pv[1]);
+        ds[qb][r >> 1] = pack_f16(dsv[0], dsv[1]);
+      }
+    // dV += P^T dO16, dK += dS^T Q16 over four 16-query steps
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int qb = ks >> 1, o = 4 * (ks & 1);
+      const half8 pa = __builtin_bit_cast(half8, make_uint4(pp[qb][o], pp[qb][o + 1], pp[qb][o + 2], pp[qb][o + 3]));
+      const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[qb][o], ds[qb][o + 1], ds[qb][o + 2], ds[qb][o + 3]));
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const half8 dob = *reinterpret_cast<const half8*>(sDT + swz_t(db * 32 + fr, 2 * ks + fk));
+        const half8 qbf = *reinterpret_cast<const half8*>(sQT + swz_t(db * 32 + fr, 2 * ks + fk));
+        dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, dob, dv[db], 0, 0, 0);
+        dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, qbf, dk[db], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- epilogue: lane = key row (fr), d = db*32 + 8*(r/4) + 4*fk + r%4 ----
+  // dV / dK accumulators are C[key][d] with key = MFMA row: lane holds col d = fr and
+  // rows key = 8*(r/4) + 4*fk + r%4. Transpose through LDS for 16-byte stores.
+  __syncthreads();
+  float* sOut = reinterpret_cast<float*>(smem);  // 128 keys x DP floats per pass (<= 4 * TILE bytes)
+  const float sk_out = ldexp1(-a - G) * p.scale, sv_out = ldexp1(-ev - G);
+  bool bad = false;
+  for (int pass = 0; pass < 2; ++pass) {
+    floatx16* acc = pass == 0 ? dv : dk;
+    const float so = pass == 0 ? sv_out : sk_out;
+    const float chk = pass == 0 ? 1.f : p.scale;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kl = wave * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+        const int d = db * 32 + fr;
+        const float x = acc[db][r];
+        if (k0 + kl < p.Sk && d < p.D) bad |= bad16(x * chk);
+        sOut[kl * DP + d] = x * so;
+      }
+    __syncthreads();
+    uint16_t* out = pass == 0 ? p.dv : p.dk;
+    for (int i = tid; i < BK * (DP / 8); i += NTH) {
+      const int kl = i / (DP / 8), d = (i % (DP / 8)) * 8;
+      const int kk = k0 + kl;
+      if (kk < p.Sk && d < p.D) {
+        const float* src = sOut + kl * DP + d;
+        stg16(out + ((int64_t)bk * p.Sk + kk) * p.D + d,
+              make_uint4(pack_bf16(src[0], src[1]), pack_bf16(src[2], src[3]), pack_bf16(src[4], src[5]),
+                         pack_bf16(src[6], src[7])));
+      }
+    }
+    __syncthreads();
+  }
+  if (bad) atomicOr(p.overflow, 1);
+}
+
+// ---- dQ --------------------------------------------------------------------------
+template <int DP, bool CAUSAL, bool HAS_BIAS>
+__global__ __launch_bounds__(NTH) void dq_kernel(BwdParams p) {
+  constexpr int BQ = 128, BKV = 64;
+  constexpr int KS = DP / 16, DB = DP / 32;
+  constexpr int TILE = BKV * DP * 2;
+  constexpr int NBLK = (BKV / 4) * (DP / 8);
+  constexpr int BL = (NBLK + NTH - 1) / NTH;
+  __shared__ __align__(16) uint8_t smem[3 * TILE];  // K, K^T, V (+ V^T slot unused)
+  uint8_t* sK = smem;
+  uint8_t* sKT = smem + TILE;
+  uint8_t* sV = smem + 2 * TILE;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, fr = lane & 31, fk = lane >> 5;
+  const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H, hk = h / (p.H / p.Hkv);
+  const int qt = CAUSAL ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;
+  const int q0 = qt * BQ;
+  const int a = p.exps_fwd[0];
+  const int ev = p.exps_fwd[2 + b * p.Hkv + hk];
+  const int G = p.exps_out[1];
+
+  const int qrow = q0 + wave * 32 + fr;
+  half8 qf[KS], df[KS];
+  {
+    const float sq = ldexp1(a), sdo = ldexp1(ev + G);
+    const uint16_t* qr = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)min(qrow, p.Sq - 1) * p.q_ss;
+    const uint16_t* dr = p.dout + (int64_t)b * p.d_sb + (int64_t)h * p.d_sh + (int64_t)min(qrow, p.Sq - 1) * p.d_ss;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int d = 16 * s + 8 * fk;
+      const bool ok = qrow < p.Sq && d < p.D;
+      qf[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(qr + d), sq) : make_uint4(0, 0, 0, 0));
+      df[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(dr + d), sdo) : make_uint4(0, 0, 0, 0));
+    }
+  }
+  const float lse_q = qrow < p.Sq ? p.lse[(int64_t)bh * p.Sq + qrow] : INFINITY;
+  const float delta_q = qrow < p.Sq ? p.delta[(int64_t)bh * p.Sq + qrow] : 0.f;
+  floatx16 dq[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
+
+  const int nkb_all = (p.Sk + BKV - 1) / BKV;
+  const int nkb = CAUSAL ? min(nkb_all, (min(q0 + BQ, p.Sq) + BKV - 1) / BKV) : nkb_all;
+  const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const uint16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
+  const float sk = ldexp1(-a), sv = ldexp1(-ev);
+  uint4 rk[BL][4], rv[BL][4];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < BL; ++i) {
+      const int blk = tid + i * NTH;
+      const int kg = blk & 15, dc = blk >> 4;
+      if (blk < NBLK) {
+        load_blk(kbase, p.k_ss, kb * BKV + 4 * kg, p.Sk, dc * 8, p.D, rk[i]);
+        load_blk(vbase, p.v_ss, kb * BKV + 4 * kg, p.Sk, dc * 8, p.D, rv[i]);
+      }
+    }
+  };
+  const uint16_t* brow = nullptr;
+  if constexpr (HAS_BIAS)
+    brow = p.bias + (int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh + (int64_t)min(qrow, p.Sq - 1) * p.bias_sq;
+
+  if (nkb > 0) gload(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < BL; ++i) {
+      const int blk = tid + i * NTH;
+      const int kg = blk & 15, dc = blk >> 4;
+      if (blk < NBLK) {
+        store_blk_both<DP>(sK, sKT, rk[i], sk, 4 * kg, dc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<uint4*>(sV + swz_row<DP>(4 * kg + r, dc)) = cvt_bf16x8_f16x8(rv[i][r], sv);
+      }
+    }
+    __syncthreads();
+    if (kb + 1 < nkb) gload(kb + 1);
+
+    // S^T and dP^T: lane = one query, 16 keys per 32-key half
+    floatx16 sacc[2], pacc[2];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[kh][r] = pacc[kh][r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const half8 ka = *reinterpret_cast<const half8*>(sK + swz_row<DP>(kh * 32 + fr, 2 * s + fk));
+        const half8 va = *reinterpret_cast<const half8*>(sV + swz_row<DP>(kh * 32 + fr, 2 * s + fk));
+        sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[s], sacc[kh], 0, 0, 0);
+        pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, df[s], pacc[kh], 0, 0, 0);
+      }
+    }
+    uint32_t ds[2][8];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float dsv[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int kk = kb * BKV + kh * 32 + 8 * ((r + u) >> 2) + 4 * fk + ((r + u) & 3);
+          float s = sacc[kh][r + u] * p.scale_log2;
+          if constexpr (HAS_BIAS) {
+            if (kk < p.Sk) s += (float)__builtin_bit_cast(_Float16, brow[kk]) * kLog2e;
+          }
+          float pr = __builtin_amdgcn_exp2f(s - lse_q);
+          if (kk >= p.Sk || qrow >= p.Sq || (CAUSAL && kk > qrow)) pr = 0.f;
+          dsv[u] = pr * (pacc[kh][r + u] - delta_q);
+        }
+        ds[kh][r >> 1] = pack_f16(dsv[0], dsv[1]);
+      }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int kh = ks >> 1, o = 4 * (ks & 1);
+      const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[kh][o], ds[kh][o + 1], ds[kh][o + 2], ds[kh][o + 3]));
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const half8 kbf = *reinterpret_cast<const half8*>(sKT + swz_t(db * 32 + fr, 2 * ks + fk));
+        dq[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbf, sa, dq[db], 0, 0, 0);
+      }
+    }
+  }
+
+  // dQ^T accumulators: lane col = query (fr), rows d = db*32 + 8*(r/4) + 4*fk + r%4
+  bool bad = false;
+  if (qrow < p.Sq) {
+    const float so = ldexp1(a - G) * p.scale;
+    const int64_t orow = ((int64_t)bh * p.Sq + qrow) * p.D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = db * 32 + 8 * rq + 4 * fk;
+        if (d >= p.D) continue;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = dq[db][4 * rq + e];
+          bad |= bad16(x * p.scale);
+          y[e] = x * so;
+        }
+        *reinterpret_cast<uint2*>(p.dq + orow + d) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+      }
+  }
+  if (bad) atomicOr(p.overflow, 1);
+}
+
+struct BwdWs {
+  int64_t nch;
+  size_t off_delta, total;
+};
+
+BwdWs bwd_ws(int64_t B, int64_t H, int64_t Sq) {
+  BwdWs w;
+  w.nch = head_amax_chunks(B * H, Sq);
+  w.off_delta = align_up((size_t)(B * H * w.nch) * 4, 256);
+  w.total = w.off_delta + align_up((size_t)(B * H * Sq) * 4, 256);
+  return w;
+}
+
+template <int DP>
+int launch_bwd_dp(const BwdParams& p, bool causal, bool has_bias, hipStream_t st) {
+  dim3 g_kv((unsigned)cdiv(p.Sk, 128), (unsigned)(p.B * p.Hkv));
+  dim3 g_q((unsigned)cdiv(p.Sq, 128), (unsigned)(p.B * p.H));
+#define LAUNCH(C, HB)                                  \
+  dkdv_kernel<DP, C, HB><<<g_kv, NTH, 0, st>>>(p);     \
+  TB_LAUNCH_CHECK("attn_bwd/dkdv");                    \
+  dq_kernel<DP, C, HB><<<g_q, NTH, 0, st>>>(p);        \
+  TB_LAUNCH_CHECK("attn_bwd/dq");
+  if (causal) {
+    if (has_bias) { LAUNCH(true, true) } else { LAUNCH(true, false) }
+  } else {
+    if (has_bias) { LAUNCH(false, true) } else { LAUNCH(false, false) }
+  }
+#undef LAUNCH
+  return 0;
+}
+
+}  // namespace
+
+extern "C" size_t tbf16_attn_bwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
+  (void)Hkv; (void)Sk; (void)D;
+  return bwd_ws(B, H, Sq).total;
+}
+
+extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const void* o16, const float* lse,
+                              const void* dout, const int32_t* exps_fwd, int64_t B, int64_t H, int64_t Hkv, int64_t Sq,
+                              int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
+                              const int64_t* v_strides, const int64_t* do_strides, const void* bias,
+                              const int64_t* bias_strides, float scale, int causal, int t_do, void* dq, void* dk,
+                              void* dv, int32_t* exps_out, int32_t* overflow, void* ws, int64_t ws_bytes,
+                              void* stream) {
+  TB_CHECK(B >= 0 && H > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0 && H % Hkv == 0, "attn_bwd: bad shape");
+  TB_CHECK(D > 0 && D % 8 == 0 && D <= 128, "attn_bwd: head dim must be a multiple of 8 up to 128");
+  TB_CHECK(q && k && v && o16 && lse && dout && exps_fwd && dq && dk && dv && exps_out && overflow,
+           "attn_bwd: null argument");
+  TB_CHECK(q_strides && k_strides && v_strides && do_strides, "attn_bwd: strides missing");
+  for (const int64_t* s : {q_strides, k_strides, v_strides, do_strides})
+    TB_CHECK(s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0, "attn_bwd: strides must be multiples of 8");
+  TB_CHECK(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dout) && aligned16(o16) && aligned16(dq) &&
+               aligned16(dk) && aligned16(dv),
+           "attn_bwd: tensors must be 16-byte aligned");
+  if (bias) TB_CHECK(bias_strides != nullptr, "attn_bwd: bias strides missing");
+  const BwdWs w = bwd_ws(B, H, Sq);
+  TB_CHECK(ws != nullptr && ws_bytes >= (int64_t)w.total, "attn_bwd: workspace too small");
+  if (B == 0 || Sq == 0 || Sk == 0) return 0;
+  hipStream_t st = as_stream(stream);
+  float* part = reinterpret_cast<float*>(ws);
+  if (int rc = launch_head_amax_partial(dout, TBF16_DT_BF16, B, H, Sq, D, do_strides[0], do_strides[1], do_strides[2],
+                                        part, w.nch, st))
+    return rc;
+  BwdParams p;
+  p.q = (const uint16_t*)q; p.k = (const uint16_t*)k; p.v = (const uint16_t*)v;
+  p.o16 = (const uint16_t*)o16; p.dout = (const uint16_t*)dout; p.lse = lse; p.exps_fwd = exps_fwd;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.d_sb = do_strides[0]; p.d_sh = do_strides[1]; p.d_ss = do_strides[2];
+  p.bias = (const uint16_t*)bias;
+  p.bias_sb = bias ? bias_strides[0] : 0; p.bias_sh = bias ? bias_strides[1] : 0; p.bias_sq = bias ? bias_strides[2] : 0;
+  p.B = (int)B; p.H = (int)H; p.Hkv = (int)Hkv; p.Sq = (int)Sq; p.Sk = (int)Sk; p.D = (int)D;
+  p.scale = scale; p.scale_log2 = scale * kLog2e; p.causal = causal; p.t_do = t_do;
+  p.part_do = part; p.nch_do = (int)w.nch;
+  p.delta = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_delta);
+  p.exps_out = exps_out; p.overflow = overflow;
+  p.dq = (uint16_t*)dq; p.dk = (uint16_t*)dk; p.dv = (uint16_t*)dv;
+  delta_kernel<<<dim3((unsigned)cdiv(Sq, 16), (unsigned)(B * H)), NTH, 0, st>>>(p);
+  TB_LAUNCH_CHECK("attn_bwd/delta");
+  if (D <= 64) return launch_bwd_dp<64>(p, causal != 0, bias != nullptr, st);
+  return launch_bwd_dp<128>(p, causal != 0, bias != nullptr, st);
+}

@@ -1,0 +1,100 @@
+// Shared device helpers for the tbf16 HIP library (gfx950 / CDNA4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tbf16 {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf162v __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ---- exponent arithmetic -------------------------------------------------
+
+__device__ __forceinline__ int exp_field(float a) { return (__float_as_int(a) >> 23) & 0xFF; }
+
+// Scale exponent p (scale = 2^p) that puts a normal amax in [2^(t-1), 2^t):
+// e = clamp(E(amax), 1, 252), se = clamp(253 + t - e, 1, 254), p = se - 127.
+// Reference: tbf16/csrc/small_kernels.cu:12-18 (gemm_sm75.cu:19-23 only differs
+// for t < 2, which the fused path never uses).
+__device__ __forceinline__ int pow2_exp(float amax, int t) {
+  int e = min(max(exp_field(amax), 1), 252);
+  int se = min(max(253 + t - e, 1), 254);
+  return se - 127;
+}
+
+// 2^p as an fp32 for p in [-126, 127] (exact, built from exponent bits).
+__device__ __forceinline__ float pow2f(int p) { return __int_as_float((p + 127) << 23); }
+
+// 2^p for any p where the result is representable (subnormals included).
+__device__ __forceinline__ float ldexp1(int p) { return __builtin_amdgcn_ldexpf(1.0f, p); }
+
+// torch.frexp exponent: x = m * 2^e with m in [0.5, 1); 0 for 0, inf and nan.
+__device__ __forceinline__ int frexp_exp(float x) { return __builtin_amdgcn_frexp_expf(x); }
+
+// ---- conversions ------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+// Two fp32 -> packed fp16, round to nearest even (v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+  half2v h = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// Two fp32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  bf162v h = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ float f16_lo(uint32_t v) {
+  return (float)__builtin_bit_cast(half2v, v)[0];
+}
+__device__ __forceinline__ float f16_hi(uint32_t v) {
+  return (float)__builtin_bit_cast(half2v, v)[1];
+}
+
+// Packed bf16 pair -> packed fp16 pair scaled by s = 2^p (exact in fp16's normal
+// range, RNE for fp16 subnormals), as quantize_rows does (small_kernels.cu:68-69).
+__device__ __forceinline__ uint32_t cvt_bf16x2_f16x2(uint32_t v, float s) {
+  return pack_f16(bf16_lo(v) * s, bf16_hi(v) * s);
+}
+
+__device__ __forceinline__ uint4 cvt_bf16x8_f16x8(uint4 v, float s) {
+  return make_uint4(cvt_bf16x2_f16x2(v.x, s), cvt_bf16x2_f16x2(v.y, s), cvt_bf16x2_f16x2(v.z, s),
+                    cvt_bf16x2_f16x2(v.w, s));
+}
+
+// ---- wave reductions (64 lanes) ----------------------------------------------
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// ---- memory ------------------------------------------------------------------
+
+__device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void stg16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+}  // namespace tbf16

@@ -1,0 +1,462 @@
+// Memory-bound kernels of the hot path: row / column power-of-two scaling and
+// quantisation to fp16, per-head amax and scale-cast, and the M = 1 GEMV.
+//
+// All of them stream HBM once (twice for the two-pass row quantiser, whose
+// second read hits L2). Loads and stores are 16 bytes per lane; one wave
+// (64 lanes) owns a row where rows are long, so reductions are in-wave.
+#include <algorithm>
+
+#include "abi_util.h"
+#include "common.h"
+
+using namespace tbf16;
+
+namespace {
+
+constexpr int kRowWaves = 4;  // rows per 256-thread block
+
+// amax (or L1 norm) of a bf16 row, reduced over the wave; valid in every lane.
+// L1 accumulates in fp64 and rounds once to fp32, so the exponent is that of the
+// exact sum (the reference's fp32 thread-order sum, small_kernels.cu:42-59, can
+// differ only within one fp32 ulp of a power of two).
+__device__ __forceinline__ float row_amax_wave(const uint16_t* xr, int K, int lane, bool l1) {
+  const uint4* p = reinterpret_cast<const uint4*>(xr);
+  const int K8 = K >> 3;
+  if (l1) {
+    double acc = 0.0;
+    for (int i = lane; i < K8; i += kWave) {
+      uint4 v = p[i];
+      acc += (double)fabsf(bf16_lo(v.x)) + (double)fabsf(bf16_hi(v.x)) + (double)fabsf(bf16_lo(v.y)) +
+             (double)fabsf(bf16_hi(v.y)) + (double)fabsf(bf16_lo(v.z)) + (double)fabsf(bf16_hi(v.z)) +
+             (double)fabsf(bf16_lo(v.w)) + (double)fabsf(bf16_hi(v.w));
+    }
+    return (float)wave_sum_d(acc);
+  }
+  float m0 = 0.f, m1 = 0.f;
+  int i = lane;
+  for (; i + kWave < K8; i += 2 * kWave) {
+    uint4 a = p[i], b = p[i + kWave];
+    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.x)), fabsf(bf16_hi(a.x))), fmaxf(fabsf(bf16_lo(a.y)), fabsf(bf16_hi(a.y)))));
+    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.z)), fabsf(bf16_hi(a.z))), fmaxf(fabsf(bf16_lo(a.w)), fabsf(bf16_hi(a.w)))));
+    m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(bf16_lo(b.x)), fabsf(bf16_hi(b.x))), fmaxf(fabsf(bf16_lo(b.y)), fabsf(bf16_hi(b.y)))));
+    m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(bf16_lo(b.z)), fabsf(bf16_hi(b.z))), fmaxf(fabsf(bf16_lo(b.w)), fabsf(bf16_hi(b.w)))));
+  }
+  if (i < K8) {
+    uint4 a = p[i];
+    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.x)), fabsf(bf16_hi(a.x))), fmaxf(fabsf(bf16_lo(a.y)), fabsf(bf16_hi(a.y)))));
+    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.z)), fabsf(bf16_hi(a.z))), fmaxf(fabsf(bf16_lo(a.w)), fabsf(bf16_hi(a.w)))));
+  }
+  return wave_max(fmaxf(m0, m1));
+}
+
+// Row exponents: one wave per row (gemm_sm75.cu:27-47 does one warp per row).
+__global__ __launch_bounds__(256) void row_exps_kernel(const uint16_t* __restrict__ x, int64_t M, int K, int64_t ldx,
+                                                       int t, int l1, int32_t* __restrict__ exps,
+                                                       float* __restrict__ s_inv) {
+  const int64_t row = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const float amax = row_amax_wave(x + row * ldx, K, lane, l1 != 0);
+  if (lane == 0) {
+    const int p = pow2_exp(amax, t);
+    if (exps) exps[row] = p;
+    if (s_inv) s_inv[row] = ldexp1(-p);
+  }
+}
+
+// quantize_rows: amax pass, then y = fp16(x * 2^p) (small_kernels.cu:35-74).
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t R, int K,
+                                                            int64_t ldx, int t, int l1, uint16_t* __restrict__ y,
+                                                            int64_t ldy, float* __restrict__ s_inv) {
+  const int64_t row = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= R) return;
+  const uint16_t* xr = x + row * ldx;
+  const float amax = row_amax_wave(xr, K, lane, l1 != 0);
+  const int p = pow2_exp(amax, t);
+  const float s = pow2f(p);
+  const uint4* src = reinterpret_cast<const uint4*>(xr);
+  uint4* dst = reinterpret_cast<uint4*>(y + row * ldy);
+  for (int i = lane; i < (K >> 3); i += kWave) dst[i] = cvt_bf16x8_f16x8(src[i], s);
+  if (lane == 0) s_inv[row] = ldexp1(-p);
+}
+
+// Transposing convert: yT[c][r] = fp16((x[r][c] * rowmul[r]) * colmul[c]) over a
+// 64 x 64 tile staged through LDS; columns r in [R, ldyT) are written as zeros so
+// that the transposed operand can be consumed with a padded contraction length.
+// rowmul = 2^rexp[r] or rm[r] (fp32) or 1; colmul = 2^cexp[c] or 1.
+__global__ __launch_bounds__(256) void transpose_convert_kernel(const uint16_t* __restrict__ x, int64_t R, int64_t K,
+                                                                int64_t ldx, const int32_t* __restrict__ rexp,
+                                                                const float* __restrict__ rm,
+                                                                const int32_t* __restrict__ cexp,
+                                                                uint16_t* __restrict__ yT, int64_t ldyT) {
+  __shared__ __align__(16) uint16_t tile[64][72];
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 64;
+  // load + convert: 64 rows x 8 chunks of 8 columns, two per thread
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rl = (tid >> 3) + 32 * i, cl = (tid & 7) * 8;
+    const int64_t r = r0 + rl, c = c0 + cl;
+    uint4 out = make_uint4(0, 0, 0, 0);
+    if (r < R && c < K) {
+      const uint4 v = ldg16(x + r * ldx + c);
+      const float rmul = rexp ? pow2f(rexp[r]) : (rm ? rm[r] : 1.f);
+      float cm[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cm[j] = cexp ? pow2f(cexp[c + j]) : 1.f;
+      out.x = pack_f16((bf16_lo(v.x) * rmul) * cm[0], (bf16_hi(v.x) * rmul) * cm[1]);
+      out.y = pack_f16((bf16_lo(v.y) * rmul) * cm[2], (bf16_hi(v.y) * rmul) * cm[3]);
+      out.z = pack_f16((bf16_lo(v.z) * rmul) * cm[4], (bf16_hi(v.z) * rmul) * cm[5]);
+      out.w = pack_f16((bf16_lo(v.w) * rmul) * cm[6], (bf16_hi(v.w) * rmul) * cm[7]);
+    }
+    *reinterpret_cast<uint4*>(&tile[rl][cl]) = out;
+  }
+  __syncthreads();
+  // write yT rows: 64 columns x 8 chunks of 8 rows
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int cl = (tid >> 3) + 32 * i, rl = (tid & 7) * 8;
+    const int64_t c = c0 + cl, r = r0 + rl;
+    if (c < K && r < ldyT) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = (uint32_t)tile[rl + 2 * j][cl] | ((uint32_t)tile[rl + 2 * j + 1][cl] << 16);
+      stg16(yT + c * ldyT + r, make_uint4(w[0], w[1], w[2], w[3]));
+    }
+  }
+}
+
+// Column amax partials: each thread covers 8 adjacent columns over a chunk of
+// rows; partial[chunk][col] (small_kernels.cu:136-155 merges with atomicMax; the
+// partials keep this pass free of a zero-fill and of atomics).
+__global__ __launch_bounds__(256) void col_amax_partial_kernel(const uint16_t* __restrict__ x, const float* __restrict__ rm,
+                                                               int64_t R, int64_t K, int64_t ldx, int64_t rows_per_chunk,
+                                                               float* __restrict__ partial) {
+  const int64_t c8 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c8 * 8 >= K) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
+  const int64_t r1 = min(R, r0 + rows_per_chunk);
+  float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t r = r0; r < r1; ++r) {
+    const uint4 v = ldg16(x + r * ldx + c8 * 8);
+    const float f = rm ? fabsf(rm[r]) : 1.f;
+    m[0] = fmaxf(m[0], fabsf(bf16_lo(v.x)) * f);
+    m[1] = fmaxf(m[1], fabsf(bf16_hi(v.x)) * f);
+    m[2] = fmaxf(m[2], fabsf(bf16_lo(v.y)) * f);
+    m[3] = fmaxf(m[3], fabsf(bf16_hi(v.y)) * f);
+    m[4] = fmaxf(m[4], fabsf(bf16_lo(v.z)) * f);
+    m[5] = fmaxf(m[5], fabsf(bf16_hi(v.z)) * f);
+    m[6] = fmaxf(m[6], fabsf(bf16_lo(v.w)) * f);
+    m[7] = fmaxf(m[7], fabsf(bf16_hi(v.w)) * f);
+  }
+  float* out = partial + (int64_t)blockIdx.y * K + c8 * 8;
+  reinterpret_cast<float4*>(out)[0] = make_float4(m[0], m[1], m[2], m[3]);
+  reinterpret_cast<float4*>(out)[1] = make_float4(m[4], m[5], m[6], m[7]);
+}
+
+// Reduce the partials of each column, then p[c] and s_inv[c] (small_kernels.cu:172,181).
+__global__ __launch_bounds__(256) void col_exps_kernel(const float* __restrict__ partial, int64_t nchunks, int64_t K,
+                                                       int t, int32_t* __restrict__ cexp, float* __restrict__ s_inv) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= K) return;
+  float m = 0.f;
+  for (int64_t i = 0; i < nchunks; ++i) m = fmaxf(m, partial[i * K + c]);
+  const int p = pow2_exp(m, t);
+  cexp[c] = p;
+  s_inv[c] = ldexp1(-p);
+}
+
+__global__ void fill_kernel(float* __restrict__ p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// ---- attention helpers --------------------------------------------------------
+
+// Per-(b, h) partial maxima of |x| over a chunk of rows: partial[bh * nchunks + chunk].
+template <typename T>
+__device__ __forceinline__ float amax8(uint4 v);
+template <>
+__device__ __forceinline__ float amax8<uint16_t>(uint4 v) {  // bf16
+  return fmaxf(fmaxf(fmaxf(fabsf(bf16_lo(v.x)), fabsf(bf16_hi(v.x))), fmaxf(fabsf(bf16_lo(v.y)), fabsf(bf16_hi(v.y)))),
+               fmaxf(fmaxf(fabsf(bf16_lo(v.z)), fabsf(bf16_hi(v.z))), fmaxf(fabsf(bf16_lo(v.w)), fabsf(bf16_hi(v.w)))));
+}
+template <>
+__device__ __forceinline__ float amax8<_Float16>(uint4 v) {  // fp16
+  return fmaxf(fmaxf(fmaxf(fabsf(f16_lo(v.x)), fabsf(f16_hi(v.x))), fmaxf(fabsf(f16_lo(v.y)), fabsf(f16_hi(v.y)))),
+               fmaxf(fmaxf(fabsf(f16_lo(v.z)), fabsf(f16_hi(v.z))), fmaxf(fabsf(f16_lo(v.w)), fabsf(f16_hi(v.w)))));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void head_amax_partial_kernel(const uint16_t* __restrict__ x, int64_t H, int64_t S,
+                                                                int64_t D, int64_t sb, int64_t sh, int64_t ss,
+                                                                int64_t rows_per_chunk, int64_t nchunks,
+                                                                float* __restrict__ partial) {
+  const int64_t bh = blockIdx.x, b = bh / H, h = bh % H;
+  const int64_t s0 = (int64_t)blockIdx.y * rows_per_chunk, s1 = min(S, s0 + rows_per_chunk);
+  const uint16_t* base = x + b * sb + h * sh;
+  const int64_t D8 = D >> 3, n = (s1 - s0) * D8;
+  float m = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 256) {
+    const int64_t s = s0 + i / D8, d = (i % D8) * 8;
+    m = fmaxf(m, amax8<T>(ldg16(base + s * ss + d)));
+  }
+  __shared__ float red[4];
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[bh * nchunks + blockIdx.y] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ void reduce_partials_kernel(const float* __restrict__ partial, int64_t n, int64_t nchunks,
+                                       float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float m = 0.f;
+  for (int64_t c = 0; c < nchunks; ++c) m = fmaxf(m, partial[i * nchunks + c]);
+  out[i] = m;
+}
+
+template <typename Tin, typename Tout>
+__device__ __forceinline__ uint4 scale_cast8(uint4 v, float sc);
+template <>
+__device__ __forceinline__ uint4 scale_cast8<uint16_t, _Float16>(uint4 v, float sc) {
+  return cvt_bf16x8_f16x8(v, sc);
+}
+template <>
+__device__ __forceinline__ uint4 scale_cast8<uint16_t, uint16_t>(uint4 v, float sc) {
+  return make_uint4(pack_bf16(bf16_lo(v.x) * sc, bf16_hi(v.x) * sc), pack_bf16(bf16_lo(v.y) * sc, bf16_hi(v.y) * sc),
+                    pack_bf16(bf16_lo(v.z) * sc, bf16_hi(v.z) * sc), pack_bf16(bf16_lo(v.w) * sc, bf16_hi(v.w) * sc));
+}
+template <>
+__device__ __forceinline__ uint4 scale_cast8<_Float16, uint16_t>(uint4 v, float sc) {
+  return make_uint4(pack_bf16(f16_lo(v.x) * sc, f16_hi(v.x) * sc), pack_bf16(f16_lo(v.y) * sc, f16_hi(v.y) * sc),
+                    pack_bf16(f16_lo(v.z) * sc, f16_hi(v.z) * sc), pack_bf16(f16_lo(v.w) * sc, f16_hi(v.w) * sc));
+}
+template <>
+__device__ __forceinline__ uint4 scale_cast8<_Float16, _Float16>(uint4 v, float sc) {
+  return make_uint4(pack_f16(f16_lo(v.x) * sc, f16_hi(v.x) * sc), pack_f16(f16_lo(v.y) * sc, f16_hi(v.y) * sc),
+                    pack_f16(f16_lo(v.z) * sc, f16_hi(v.z) * sc), pack_f16(f16_lo(v.w) * sc, f16_hi(v.w) * sc));
+}
+
+// y (contiguous) = x * 2^e[b, h] (small_kernels.cu:246-263). The scale is built
+// with ldexp so any int32 exponent that keeps the result representable works.
+template <typename Tin, typename Tout>
+__global__ __launch_bounds__(256) void head_scale_cast_kernel(const uint16_t* __restrict__ x, int64_t H, int64_t S,
+                                                              int64_t D, int64_t sb, int64_t sh, int64_t ss,
+                                                              const int32_t* __restrict__ e, int64_t e_sb,
+                                                              int64_t e_sh, uint16_t* __restrict__ y, int64_t total8) {
+  const int64_t D8 = D >> 3;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total8; i += (int64_t)gridDim.x * 256) {
+    const int64_t d = (i % D8) * 8, row = i / D8, s = row % S, bh = row / S, b = bh / H, h = bh % H;
+    const float sc = ldexp1(e[b * e_sb + h * e_sh]);
+    stg16(y + i * 8, scale_cast8<Tin, Tout>(ldg16(x + b * sb + h * sh + s * ss + d), sc));
+  }
+}
+
+// M = 1 GEMV (small_kernels.cu:107-132): one wave per output, fp32 FMA on bf16 x
+// and fp16 w, no activation scale.
+__global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                   const float* __restrict__ ws, const uint16_t* __restrict__ bias,
+                                                   uint16_t* __restrict__ y, int64_t N, int K, int64_t ldw) {
+  const int64_t n = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;
+  const uint4* xr = reinterpret_cast<const uint4*>(x);
+  const uint4* wr = reinterpret_cast<const uint4*>(w + n * ldw);
+  float a0 = 0.f, a1 = 0.f;
+  const int K8 = K >> 3;
+  for (int i = lane; i < K8; i += kWave) {
+    const uint4 xv = xr[i], wv = wr[i];
+    a0 = fmaf(bf16_lo(xv.x), f16_lo(wv.x), a0);
+    a1 = fmaf(bf16_hi(xv.x), f16_hi(wv.x), a1);
+    a0 = fmaf(bf16_lo(xv.y), f16_lo(wv.y), a0);
+    a1 = fmaf(bf16_hi(xv.y), f16_hi(wv.y), a1);
+    a0 = fmaf(bf16_lo(xv.z), f16_lo(wv.z), a0);
+    a1 = fmaf(bf16_hi(xv.z), f16_hi(wv.z), a1);
+    a0 = fmaf(bf16_lo(xv.w), f16_lo(wv.w), a0);
+    a1 = fmaf(bf16_hi(xv.w), f16_hi(wv.w), a1);
+  }
+  const float acc = wave_sum(a0 + a1);
+  if (lane == 0) {
+    float r = acc * ws[n];
+    if (bias) r += bf16_lo(bias[n]);
+    const uint32_t packed = pack_bf16(r, 0.f);
+    y[n] = (uint16_t)(packed & 0xffffu);
+  }
+}
+
+int check_rows(const char* fn, const void* x, int64_t R, int64_t K, int64_t ldx) {
+  TB_CHECK(x != nullptr || R * K == 0, "%s: null input", fn);
+  TB_CHECK(R >= 0 && K >= 0, "%s: negative shape", fn);
+  TB_CHECK(K % 8 == 0 && ldx % 8 == 0 && ldx >= K && aligned16(x),
+           "%s: K and row stride must be multiples of 8", fn);
+  TB_CHECK(K < (int64_t)1 << 31, "%s: K too large", fn);
+  return 0;
+}
+
+int64_t col_chunks(int64_t R, int64_t K) {
+  const int64_t col_blocks = cdiv(cdiv(K, 8), 256);
+  int64_t chunks = cdiv(1024, col_blocks);
+  chunks = std::max<int64_t>(1, std::min<int64_t>(chunks, cdiv(R, 32)));
+  return chunks;
+}
+
+int64_t head_chunks(int64_t BH, int64_t S) {
+  return std::max<int64_t>(1, std::min<int64_t>(cdiv(2048, std::max<int64_t>(BH, 1)), cdiv(S, 32)));
+}
+
+}  // namespace
+
+// Shared with attention.hip: partial head maxima in one launch per tensor.
+namespace tbf16 {
+int64_t head_amax_chunks(int64_t BH, int64_t S) { return head_chunks(BH, S); }
+
+int launch_head_amax_partial(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                             int64_t sh, int64_t ss, float* partial, int64_t nchunks, hipStream_t st) {
+  const int64_t rows = cdiv(S, nchunks);
+  dim3 grid((unsigned)(B * H), (unsigned)nchunks);
+  if (dtype == TBF16_DT_BF16)
+    head_amax_partial_kernel<uint16_t><<<grid, 256, 0, st>>>((const uint16_t*)x, H, S, D, sb, sh, ss, rows, nchunks,
+                                                             partial);
+  else
+    head_amax_partial_kernel<_Float16><<<grid, 256, 0, st>>>((const uint16_t*)x, H, S, D, sb, sh, ss, rows, nchunks,
+                                                             partial);
+  TB_LAUNCH_CHECK("head_amax");
+  return 0;
+}
+
+int launch_row_exps(const void* x, int64_t M, int64_t K, int64_t ldx, int t, int l1, int32_t* exps, float* s_inv,
+                    hipStream_t st) {
+  if (M == 0) return 0;
+  row_exps_kernel<<<(unsigned)cdiv(M, kRowWaves), 256, 0, st>>>((const uint16_t*)x, M, (int)K, ldx, t, l1, exps, s_inv);
+  TB_LAUNCH_CHECK("row_exps");
+  return 0;
+}
+}  // namespace tbf16
+
+extern "C" int tbf16_row_exps(const void* x, int64_t M, int64_t K, int64_t ldx, int t, int l1, int32_t* exps,
+                              float* s_inv, void* stream) {
+  if (int rc = check_rows("row_exps", x, M, K, ldx)) return rc;
+  TB_CHECK(exps != nullptr || s_inv != nullptr, "row_exps: no output");
+  return launch_row_exps(x, M, K, ldx, t, l1, exps, s_inv, as_stream(stream));
+}
+
+extern "C" int tbf16_quantize_rows(const void* x, int64_t R, int64_t K, int64_t ldx, int t, int l1, void* y16,
+                                   int64_t ldy, float* s_inv, void* stream) {
+  if (int rc = check_rows("quantize_rows", x, R, K, ldx)) return rc;
+  TB_CHECK(ldy % 8 == 0 && ldy >= K && aligned16(y16) && s_inv, "quantize_rows: bad output");
+  if (R == 0) return 0;
+  quantize_rows_kernel<<<(unsigned)cdiv(R, kRowWaves), 256, 0, as_stream(stream)>>>(
+      (const uint16_t*)x, R, (int)K, ldx, t, l1, (uint16_t*)y16, ldy, s_inv);
+  TB_LAUNCH_CHECK("quantize_rows");
+  return 0;
+}
+
+extern "C" int tbf16_quantize_rows_t(const void* x, int64_t R, int64_t K, int64_t ldx, int t, void* yT, int64_t ldyT,
+                                     float* s_inv, int32_t* exps_ws, void* stream) {
+  if (int rc = check_rows("quantize_rows_t", x, R, K, ldx)) return rc;
+  TB_CHECK(ldyT % 8 == 0 && ldyT >= R && aligned16(yT) && s_inv && exps_ws, "quantize_rows_t: bad output");
+  hipStream_t st = as_stream(stream);
+  if (R > 0) {
+    if (int rc = launch_row_exps(x, R, K, ldx, t, 0, exps_ws, s_inv, st)) return rc;
+  }
+  if (K == 0 || ldyT == 0) return 0;
+  dim3 grid((unsigned)cdiv(K, 64), (unsigned)cdiv(ldyT, 64));
+  transpose_convert_kernel<<<grid, 256, 0, st>>>((const uint16_t*)x, R, K, ldx, exps_ws, nullptr, nullptr,
+                                                 (uint16_t*)yT, ldyT);
+  TB_LAUNCH_CHECK("quantize_rows_t");
+  return 0;
+}
+
+extern "C" size_t tbf16_quantize_cols_ws_bytes(int64_t R, int64_t K) {
+  const int64_t ch = col_chunks(R, K);
+  return align_up((size_t)(ch * K) * sizeof(float), 256) + align_up((size_t)K * sizeof(int32_t), 256);
+}
+
+extern "C" int tbf16_quantize_cols_t(const void* x, int64_t R, int64_t K, int64_t ldx, int t, const float* row_mul,
+                                     void* yT, int64_t ldyT, float* s_inv, void* ws, int64_t ws_bytes, void* stream) {
+  if (int rc = check_rows("quantize_cols", x, R, K, ldx)) return rc;
+  TB_CHECK(ldyT % 8 == 0 && ldyT >= R && aligned16(yT) && s_inv, "quantize_cols: bad output");
+  TB_CHECK(ws != nullptr && ws_bytes >= (int64_t)tbf16_quantize_cols_ws_bytes(R, K), "quantize_cols: workspace too small");
+  hipStream_t st = as_stream(stream);
+  if (K == 0) return 0;
+  const int64_t ch = col_chunks(R, K);
+  float* partial = reinterpret_cast<float*>(ws);
+  int32_t* cexp = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(ws) + align_up((size_t)(ch * K) * sizeof(float), 256));
+  if (R > 0) {
+    dim3 g1((unsigned)cdiv(cdiv(K, 8), 256), (unsigned)ch);
+    col_amax_partial_kernel<<<g1, 256, 0, st>>>((const uint16_t*)x, row_mul, R, K, ldx, cdiv(R, ch), partial);
+    TB_LAUNCH_CHECK("quantize_cols/amax");
+    col_exps_kernel<<<(unsigned)cdiv(K, 256), 256, 0, st>>>(partial, ch, K, t, cexp, s_inv);
+    TB_LAUNCH_CHECK("quantize_cols/exps");
+  } else {  // no rows: s_inv = 1 as the reference returns (small_kernels.cu:325)
+    fill_kernel<<<(unsigned)cdiv(K, 256), 256, 0, st>>>(s_inv, K, 1.0f);
+    TB_LAUNCH_CHECK("quantize_cols/fill");
+  }
+  if (ldyT == 0) return 0;
+  dim3 grid((unsigned)cdiv(K, 64), (unsigned)cdiv(ldyT, 64));
+  transpose_convert_kernel<<<grid, 256, 0, st>>>((const uint16_t*)x, R, K, ldx, nullptr, row_mul, cexp, (uint16_t*)yT,
+                                                 ldyT);
+  TB_LAUNCH_CHECK("quantize_cols/convert");
+  return 0;
+}
+
+extern "C" int tbf16_gemv(const void* x, const void* w16, int64_t N, int64_t K, int64_t ldw, const float* ws,
+                          const void* bias, void* y, void* stream) {
+  TB_CHECK(K % 8 == 0 && ldw % 8 == 0 && ldw >= K && aligned16(x) && aligned16(w16), "gemv: K and row stride must be multiples of 8");
+  TB_CHECK(ws && y, "gemv: bad arguments");
+  if (N == 0) return 0;
+  gemv_kernel<<<(unsigned)cdiv(N, kRowWaves), 256, 0, as_stream(stream)>>>(
+      (const uint16_t*)x, (const uint16_t*)w16, ws, (const uint16_t*)bias, (uint16_t*)y, N, (int)K, ldw);
+  TB_LAUNCH_CHECK("gemv");
+  return 0;
+}
+
+extern "C" int tbf16_head_amax(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                               int64_t sh, int64_t ss, float* out, void* stream) {
+  TB_CHECK(dtype == TBF16_DT_BF16 || dtype == TBF16_DT_F16, "head_amax: bf16 or fp16");
+  TB_CHECK(D % 8 == 0 && sb % 8 == 0 && sh % 8 == 0 && ss % 8 == 0 && aligned16(x),
+           "expected (B, H, S, D) with contiguous D %% 8 == 0");
+  TB_CHECK(out != nullptr, "head_amax: null output");
+  const int64_t BH = B * H;
+  if (BH == 0) return 0;
+  hipStream_t st = as_stream(stream);
+  TB_CHECK(S > 0 && D > 0, "head_amax: empty heads are handled by the caller");
+  // One block per head writes its maximum straight into out (no partials, no
+  // zero-fill). The fused attention path uses the chunked partial launch instead.
+  const int64_t nchunks = 1;
+  const int64_t rows = S;
+  dim3 grid((unsigned)BH, (unsigned)nchunks);
+  if (dtype == TBF16_DT_BF16)
+    head_amax_partial_kernel<uint16_t><<<grid, 256, 0, st>>>((const uint16_t*)x, H, S, D, sb, sh, ss, rows, nchunks, out);
+  else
+    head_amax_partial_kernel<_Float16><<<grid, 256, 0, st>>>((const uint16_t*)x, H, S, D, sb, sh, ss, rows, nchunks, out);
+  TB_LAUNCH_CHECK("head_amax");
+  return 0;
+}
+
+extern "C" int tbf16_head_scale_cast(const void* x, int in_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                                     int64_t sb, int64_t sh, int64_t ss, const int32_t* e, int64_t e_sb, int64_t e_sh,
+                                     void* y, int out_dtype, void* stream) {
+  TB_CHECK((in_dtype == TBF16_DT_BF16 || in_dtype == TBF16_DT_F16) &&
+               (out_dtype == TBF16_DT_BF16 || out_dtype == TBF16_DT_F16),
+           "head_scale_cast: bf16/fp16 only");
+  TB_CHECK(D % 8 == 0 && sb % 8 == 0 && sh % 8 == 0 && ss % 8 == 0 && aligned16(x) && aligned16(y),
+           "expected (B, H, S, D) with contiguous D %% 8 == 0");
+  const int64_t total8 = B * H * S * D / 8;
+  if (total8 == 0) return 0;
+  const unsigned blocks = (unsigned)std::min<int64_t>(cdiv(total8, 256), 256 * 16);
+  hipStream_t st = as_stream(stream);
+#define LAUNCH(TI, TO)                                                                                           \
+  head_scale_cast_kernel<TI, TO><<<blocks, 256, 0, st>>>((const uint16_t*)x, H, S, D, sb, sh, ss, e, e_sb, e_sh, \
+                                                         (uint16_t*)y, total8)
+  if (in_dtype == TBF16_DT_BF16 && out_dtype == TBF16_DT_F16) LAUNCH(uint16_t, _Float16);
+  else if (in_dtype == TBF16_DT_F16 && out_dtype == TBF16_DT_BF16) LAUNCH(_Float16, uint16_t);
+  else if (in_dtype == TBF16_DT_BF16) LAUNCH(uint16_t, uint16_t);
+  else LAUNCH(_Float16, _Float16);
+#undef LAUNCH
+  TB_LAUNCH_CHECK("head_scale_cast");
+  return 0;
+}
