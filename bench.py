@@ -1,0 +1,283 @@
+"""Benchmark of the scaled-fp16 hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+
+Headline (BASELINE.json metric, configs[1]): the 4096^3 scaled GEMM. One step =
+one tbf16.scaled_linear call on resident bf16 inputs: the row-exponent pre-pass
+plus the fused MFMA GEMM, exactly what a caller runs (prepare_weight is done once,
+outside the timed region, as the reference's benchmark does). `value` is TFLOPS
+over K steps timed with HIP events between two synchronizations.
+
+Also measured (same JSON line): the 16k-token causal scaled attention forward
+(configs[3]) and its 4k variant, the small-M decode sweep in HBM GB/s (configs[2],
+weights rotated over > 256 MB so the MALL cannot hold them), and the training
+step of configs[4]. `roofline` prices the dominant kernel (the GEMM) against the
+dense fp16 MFMA peak from its own event-timed launches; `cpu_baseline` times the
+oracle's restatement of the same workload on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "turing-bf16_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+PEAK_FP16_TFLOPS = 2516.6   # 256 CU x 4096 FLOP/clk x 2.4 GHz, dense
+PEAK_HBM_GBS = 8000.0
+
+
+def _baseline():
+    with open(ROOT / "BASELINE.json") as f:
+        return json.load(f)
+
+
+def _events_time(fn, iters: int) -> float:
+    """Mean milliseconds per call of fn, HIP events on torch's current stream (the
+    stream every tbf16 kernel is launched on)."""
+    import torch
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def bench_gemm(steps: int, warmup: int):
+    import torch
+    import tbf16
+    from tbf16 import _ext
+    import workloads as W
+
+    dev = torch.device("cuda", 0)
+    x, w, _ = W.cfg2_square_gemm()
+    x, w = x.to(dev), w.to(dev)
+    w16, ws = tbf16.prepare_weight(w)
+    M, K = x.shape
+    N = w16.shape[0]
+    flops = 2.0 * M * N * K
+    for _ in range(warmup):
+        tbf16.scaled_linear(x, w16, ws)
+    torch.cuda.synchronize()
+    # the timed region: K steps, synchronized on both sides
+    t0 = time.perf_counter()
+    ms = _events_time(lambda: tbf16.scaled_linear(x, w16, ws), steps)
+    wall = time.perf_counter() - t0
+    # the dominant kernel alone: GEMM launches with precomputed row exponents
+    exps = torch.empty(M, dtype=torch.int32, device=dev)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    st = _ext.stream()
+    _ext.call("tbf16_row_exps", x.data_ptr(), M, K, K, 15, 0, exps.data_ptr(), None, st)
+
+    def gemm_only():
+        _ext.call("tbf16_linear_exps", x.data_ptr(), M, K, K, exps.data_ptr(), w16.data_ptr(), N, K, ws.data_ptr(),
+                  None, y.data_ptr(), N, -1, st)
+
+    for _ in range(3):
+        gemm_only()
+    gemm_ms = _events_time(gemm_only, max(steps, 20))
+
+    def rows_only():
+        _ext.call("tbf16_row_exps", x.data_ptr(), M, K, K, 15, 0, exps.data_ptr(), None, st)
+
+    rows_ms = _events_time(rows_only, max(steps, 20))
+    return {"ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12, "gemm_ms": gemm_ms,
+            "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12, "rowscale_ms": rows_ms,
+            "rowscale_gbs": M * K * 2 / (rows_ms * 1e-3) / 1e9, "flops": flops, "wall_s": wall}
+
+
+def bench_attention(S: int, iters: int):
+    import torch
+    import tbf16
+    import workloads as W
+
+    dev = torch.device("cuda", 0)
+    q, k, v = (t.to(dev) for t in W.cfg4_attention(S))
+    B, H, _, D = q.shape
+    flops = 2.0 * B * H * S * S * D  # causal: half of 4 B H S^2 D
+    for _ in range(2):
+        tbf16.sdpa(q, k, v, is_causal=True)
+    ms = _events_time(lambda: tbf16.sdpa(q, k, v, is_causal=True), iters)
+    return {"S": S, "ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "pct_peak": 100 * flops / (ms * 1e-3) / 1e12 /
+            PEAK_FP16_TFLOPS}
+
+
+def bench_small_m(iters: int):
+    import torch
+    import tbf16
+    import workloads as W
+
+    dev = torch.device("cuda", 0)
+    w, xs = W.cfg3_small_m()
+    N, K = w.shape
+    w16, ws = tbf16.prepare_weight(w.to(dev))
+    copies = 7  # 7 x 52 MB > 256 MB MALL
+    ws16 = [w16.clone() for _ in range(copies)]
+    out = {}
+    for M, x in xs.items():
+        xd = x.to(dev)
+        i = [0]
+
+        def step():
+            tbf16.scaled_linear(xd, ws16[i[0] % copies], ws)
+            i[0] += 1
+
+        for _ in range(copies):
+            step()
+        ms = _events_time(step, iters * copies)
+        byt = 2 * N * K + 2 * M * K + 2 * M * N + 4 * N + 4 * M
+        out[str(M)] = {"us": round(ms * 1e3, 2), "GBs": round(byt / (ms * 1e-3) / 1e9, 1),
+                       "pct_hbm": round(100 * byt / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+                       "tflops": round(2 * M * N * K / (ms * 1e-3) / 1e12, 2)}
+    return out
+
+
+def bench_train(iters: int):
+    import torch
+    import tbf16.autograd as ag
+    import workloads as W
+
+    dev = torch.device("cuda", 0)
+    x, w, dy = (t.to(dev) for t in W.cfg5_train_linear())
+    M, K = x.shape
+    N = w.shape[0]
+    xg, wg = x.clone().requires_grad_(), w.clone().requires_grad_()
+
+    def lin():
+        xg.grad = wg.grad = None
+        ag.linear(xg, wg).backward(dy)
+
+    lin()
+    lin_ms = _events_time(lin, iters)
+    q, k, v, do = (t.to(dev) for t in W.cfg5_train_attention())
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+
+    def att():
+        qg.grad = kg.grad = vg.grad = None
+        ag.sdpa(qg, kg, vg, is_causal=True).backward(do)
+
+    att()
+    att_ms = _events_time(att, iters)
+    B, H, S, D = q.shape
+    lin_fl = 6.0 * M * K * N
+    att_fl = 2.0 * B * H * S * S * D * 3.5  # fwd + bwd ~ 3.5x the causal forward (tests/test_autograd.py:108)
+    return {"linear_ms": round(lin_ms, 3), "linear_tflops": round(lin_fl / (lin_ms * 1e-3) / 1e12, 1),
+            "attention_ms": round(att_ms, 3), "attention_tflops": round(att_fl / (att_ms * 1e-3) / 1e12, 1),
+            "step_ms": round(lin_ms + att_ms, 3),
+            "step_tflops": round((lin_fl + att_fl) / ((lin_ms + att_ms) * 1e-3) / 1e12, 1)}
+
+
+def cpu_baseline():
+    """The oracle's restatement of the fused scaled linear (quantise rows, fp32
+    matmul, scale, one bf16 rounding) on the full 4096^3 config, on the host cores."""
+    import torch
+    import workloads as W
+    from oracle import tbf16_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    x, w, _ = W.cfg2_square_gemm()
+    w16, ws = O.prepare_weight(w)  # once, outside the timing (as on the GPU)
+    O.linear_fused(x[:64], w16, ws)
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        O.linear_fused(x, w16, ws)
+        times.append(time.perf_counter() - t)
+    sec = statistics.median(times)
+    fl = 2.0 * 4096 ** 3
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(fl / sec / 1e12, 4), "unit": "TFLOPS", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"full 4096^3 scaled GEMM restatement (oracle.linear_fused: fp32 matmul), median of 3 runs, "
+                      f"{sec:.2f} s each, {cpu_model}"}
+
+
+def traffic_from_profiles():
+    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary (FETCH_SIZE
+    and WRITE_SIZE, calibrated against a copy kernel), if present."""
+    p = ROOT / "profiles" / "gemm_4096_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline GEMM only")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the scaled-fp16 path has no multi-GPU component); "
+              "use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    base = _baseline()
+    g = bench_gemm(a.steps, a.warmup)
+    print(f"[bench] gemm 4096^3: {g['tflops']:.1f} TFLOPS/step, kernel {g['gemm_tflops']:.1f} TFLOPS", file=sys.stderr,
+          flush=True)
+    extras = {}
+    if not a.quick:
+        extras["attention_fwd"] = [bench_attention(S, it) for S, it in ((4096, 20), (16384, 5))]
+        print(f"[bench] attention {extras['attention_fwd']}", file=sys.stderr, flush=True)
+        extras["small_m_decode"] = bench_small_m(20)
+        print(f"[bench] small-M {extras['small_m_decode']}", file=sys.stderr, flush=True)
+        extras["train_step"] = bench_train(5)
+        print(f"[bench] train {extras['train_step']}", file=sys.stderr, flush=True)
+    achieved = g["gemm_tflops"]
+    line = {
+        "metric": base["metric"],
+        "value": round(g["tflops"], 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(g["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (configs[1]: rows N(0,1)*2^e, e in [-20,20], seed 0; bf16 in, bf16 out)",
+        "config": {"workload": "4096^3 scaled GEMM (BASELINE configs[1]): row-scale pre-pass + fused fp16 MFMA GEMM",
+                   "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
+        "pct_fp16_peak": round(100 * g["tflops"] / PEAK_FP16_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic_from_profiles(),
+                     "kernel": "gemm_kernel<256,256,4,2,bf16 a> (tbf16_linear_exps)",
+                     "kernel_us": round(g["gemm_ms"] * 1e3, 2),
+                     "algorithmic_flops_per_launch": g["flops"]},
+        "rowscale_prepass": {"us": round(g["rowscale_ms"] * 1e3, 2), "GBs": round(g["rowscale_gbs"], 1)},
+    }
+    line.update(extras)
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
