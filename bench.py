@@ -209,6 +209,34 @@ def cpu_baseline():
                       f"{sec:.2f} s each, {cpu_model}"}
 
 
+def profile_run(what: str):
+    """A few launches of one workload, for rocprofv3 counter passes."""
+    import torch
+    import tbf16
+    import workloads as W
+
+    dev = torch.device("cuda", 0)
+    if what == "gemm":
+        x, w, _ = W.cfg2_square_gemm()
+        x, w = x.to(dev), w.to(dev)
+        w16, ws = tbf16.prepare_weight(w)
+        for _ in range(5):
+            tbf16.scaled_linear(x, w16, ws)
+        a = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)  # 256 MiB
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+    elif what == "attention":
+        for S in (4096, 16384):
+            q, k, v = (t.to(dev) for t in W.cfg4_attention(S))
+            for _ in range(3):
+                tbf16.sdpa(q, k, v, is_causal=True)
+    else:
+        bench_small_m(2)
+    torch.cuda.synchronize()
+    print(f"profile run done: {what}", flush=True)
+
+
 def traffic_from_profiles():
     """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary (FETCH_SIZE
     and WRITE_SIZE, calibrated against a copy kernel), if present."""
@@ -228,6 +256,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline GEMM only")
+    ap.add_argument("--profile", choices=["gemm", "attention", "small_m"], default=None,
+                    help="run a few launches of one workload for rocprofv3 and exit (no JSON); 'gemm' also runs a "
+                         "256 MiB device copy that calibrates FETCH_SIZE / WRITE_SIZE")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the scaled-fp16 path has no multi-GPU component); "
@@ -237,6 +268,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if a.profile:
+        profile_run(a.profile)
+        return
     base = _baseline()
     g = bench_gemm(a.steps, a.warmup)
     print(f"[bench] gemm 4096^3: {g['tflops']:.1f} TFLOPS/step, kernel {g['gemm_tflops']:.1f} TFLOPS", file=sys.stderr,

@@ -15,9 +15,14 @@
 //    barrier per k tile. LDS rows are 128 bytes (64 fp16) with the 16-byte chunk
 //    index XOR-swizzled by (row / 2) % 8, so the 32-row fragment reads
 //    (ds_read_b128) and the 8-lanes-per-row stores are bank-conflict free.
+//  - two register sets alternate (loop unrolled by two), so each k tile's global
+//    loads are issued two compute phases before they are needed; tiles that are
+//    full in M, N and K use unpredicated loads.
 //  - the MFMA's first operand is the b fragment, the second the a fragment, so a
-//    lane's 16 accumulators are four runs of 4 consecutive n for one m: the
-//    epilogue writes 8-byte bf16 runs straight from registers (one rounding).
+//    lane's 16 accumulators are four runs of 4 consecutive n for one m. The
+//    epilogue rounds once to bf16, stages the tile rows in LDS and writes each
+//    row as contiguous 16-byte lanes (register-direct 8-byte stores were
+//    written back in partial sectors, ~5x the output bytes).
 //  - block ids are remapped so that each XCD (8 per chip, round-robin dispatch)
 //    gets a contiguous range of tiles, grouped 8 a-tiles deep for L2 reuse.
 #include <algorithm>
@@ -29,11 +34,46 @@ using namespace tbf16;
 
 namespace {
 
-constexpr int BK = 64;
+// Byte offset of 16-byte chunk `chunk` of row `row` in a [rows][BK] fp16 tile.
+// BK = 64: 128-byte rows, chunk ^= (row / 2) % 8; BK = 32: 64-byte rows,
+// chunk ^= (row / 4) % 4. Either way 16 lanes reading 16 consecutive rows at one
+// logical chunk, or 8 (4) lanes writing one row, touch 64 distinct banks.
+template <int BK>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  if constexpr (BK == 64) return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
+  else return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
+}
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+typedef int int4v __attribute__((ext_vector_type(4)));
 
-template <int BM, int BN, int WM, int WN, bool A_BF16>
+// The raw buffer load intrinsic with a 4 x i32 resource (this form keeps the
+// descriptor in SGPRs; the pointer-typed builtin lost uniformity through the
+// staging lambdas and produced a waterfall loop around every load).
+__device__ int4v raw_buffer_load_b128(int4v rsrc, int voffset, int soffset, int aux) __asm(
+    "llvm.amdgcn.raw.buffer.load.v4i32");
+
+// Raw buffer resource over [p, p + bytes): loads past the end return zeros.
+// Dword 3 = 0x00020000 is the gfx9-family raw-buffer format word.
+struct BufRes {
+  int lo, hi, bytes;
+};
+__device__ __forceinline__ BufRes make_res(const void* p, int64_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return BufRes{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes};
+}
+// 16-byte buffer load; the descriptor is rebuilt from scalars at the use so the
+// compiler keeps it in SGPRs (a descriptor it cannot prove uniform costs a
+// waterfall loop per load and breaks its wait-count tracking).
+__device__ __forceinline__ uint4 buf_load16(BufRes r, int voffset, int soffset) {
+  int4v d;
+  d.x = __builtin_amdgcn_readfirstlane(r.lo);
+  d.y = __builtin_amdgcn_readfirstlane(r.hi);
+  d.z = __builtin_amdgcn_readfirstlane(r.bytes);
+  d.w = 0x00020000;
+  return __builtin_bit_cast(uint4, raw_buffer_load_b128(d, voffset, __builtin_amdgcn_readfirstlane(soffset), 0));
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int PF, bool A_BF16, bool EVEN>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                            const int32_t* __restrict__ a_exp,
                                                            const float* __restrict__ a_sinv,
@@ -44,11 +84,19 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   constexpr int NT = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
-  constexpr int RP = NT / 8;  // rows covered by one pass of 16-byte loads (8 lanes per 128-byte row)
+  constexpr int CPR = BK / 8;  // 16-byte chunks per tile row
+  constexpr int RP = NT / CPR;  // rows covered by one pass of 16-byte loads
   constexpr int AL = BM / RP, BL = BN / RP;
   static_assert(FM >= 1 && FN >= 1 && AL * RP == BM && BL * RP == BN, "bad tile");
-  constexpr int STAGE = (BM + BN) * 128;
-  __shared__ __align__(16) uint8_t smem[2 * STAGE];
+  constexpr int RB = BK * 2;  // bytes per LDS tile row
+  constexpr int STAGE = (BM + BN) * RB;
+  // epilogue staging: tile rows of PITCH bytes, in passes of RPP rows (>= one wave's rows)
+  constexpr int PITCH = BN * 2 + 16;
+  constexpr int PFIT = (BM * PITCH <= 2 * STAGE) ? 1 : (BM / 2 * PITCH <= 2 * STAGE) ? 2 : 4;
+  constexpr int PASSES = PFIT < BM / TM ? PFIT : BM / TM;
+  constexpr int RPP = BM / PASSES;
+  constexpr int SMEM = 2 * STAGE > RPP * PITCH ? 2 * STAGE : RPP * PITCH;
+  __shared__ __align__(16) uint8_t smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -64,44 +112,51 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   const int m0 = (first + within % gsize) * BM;
   const int n0 = (within / gsize) * BN;
 
-  // ---- global -> register staging ----
-  const int lrow = tid >> 3, lch = tid & 7;
-  const uint16_t* ga[AL];
-  const uint16_t* gb[BL];
-  bool aok[AL], bok[BL];
+  // ---- global -> register staging through buffer loads ----
+  // One buffer resource per operand tile (SGPRs), loop-invariant 32-bit row
+  // offsets (VGPRs) and the k offset in an SGPR: no per-iteration address math
+  // in vector registers, so in-flight loads of other register sets are never
+  // waited for early. Rows past M (N) lie past the resource's end and load as
+  // zeros; a K tail (K % BK != 0) is zeroed by a select.
+  const int lrow = tid / CPR, lch = tid % CPR;
+  const BufRes arsrc = make_res(A + (int64_t)m0 * lda, min<int64_t>((int64_t)(M - m0) * lda * 2, 0x7fffffff));
+  const BufRes brsrc = make_res(B + (int64_t)n0 * ldb, min<int64_t>((int64_t)(N - n0) * ldb * 2, 0x7fffffff));
+  int aoff[AL], boff[BL];
   float as[AL];
 #pragma unroll
   for (int i = 0; i < AL; ++i) {
-    const int r = m0 + lrow + i * RP;
-    aok[i] = r < M;
-    ga[i] = A + (int64_t)(aok[i] ? r : 0) * lda + lch * 8;
-    if constexpr (A_BF16) as[i] = aok[i] ? pow2f(a_exp[r]) : 0.f;
+    const int r = lrow + i * RP;
+    aoff[i] = (r * (int)lda + lch * 8) * 2;
+    if constexpr (A_BF16) as[i] = (EVEN || m0 + r < M) ? pow2f(a_exp[m0 + r]) : 0.f;
   }
 #pragma unroll
-  for (int i = 0; i < BL; ++i) {
-    const int r = n0 + lrow + i * RP;
-    bok[i] = r < N;
-    gb[i] = B + (int64_t)(bok[i] ? r : 0) * ldb + lch * 8;
-  }
-  uint4 ra[AL], rb[BL];
-  auto gload = [&](int kt) {
-    const bool kok = kt * BK + lch * 8 < K;
+  for (int i = 0; i < BL; ++i) boff[i] = ((lrow + i * RP) * (int)ldb + lch * 8) * 2;
+  uint4 ra[PF][AL], rb[PF][BL];
+  auto gload = [&](uint4(&va)[AL], uint4(&vb)[BL], int kt) {
+    const int koff = kt * BK * 2;
+    const bool kok = EVEN || kt * BK + lch * 8 < K;
 #pragma unroll
-    for (int i = 0; i < AL; ++i) ra[i] = (kok && aok[i]) ? ldg16(ga[i] + kt * BK) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < AL; ++i) {
+      const uint4 v = buf_load16(arsrc, aoff[i], koff);
+      va[i] = kok ? v : make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
-    for (int i = 0; i < BL; ++i) rb[i] = (kok && bok[i]) ? ldg16(gb[i] + kt * BK) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < BL; ++i) {
+      const uint4 v = buf_load16(brsrc, boff[i], koff);
+      vb[i] = kok ? v : make_uint4(0, 0, 0, 0);
+    }
   };
-  auto lstore = [&](int stg) {
+  auto lstore = [&](const uint4(&ra)[AL], const uint4(&rb)[BL], int stg) {
     uint8_t* sA = smem + stg * STAGE;
-    uint8_t* sB = sA + BM * 128;
+    uint8_t* sB = sA + BM * RB;
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
       uint4 v = ra[i];
       if constexpr (A_BF16) v = cvt_bf16x8_f16x8(v, as[i]);
-      *reinterpret_cast<uint4*>(sA + swz(lrow + i * RP, lch)) = v;
+      *reinterpret_cast<uint4*>(sA + swz<BK>(lrow + i * RP, lch)) = v;
     }
 #pragma unroll
-    for (int i = 0; i < BL; ++i) *reinterpret_cast<uint4*>(sB + swz(lrow + i * RP, lch)) = rb[i];
+    for (int i = 0; i < BL; ++i) *reinterpret_cast<uint4*>(sB + swz<BK>(lrow + i * RP, lch)) = rb[i];
   };
 
   floatx16 acc[FN][FM];
@@ -115,15 +170,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   const int fr = lane & 31, fk = lane >> 5;
   auto compute = [&](int stg) {
     const uint8_t* sA = smem + stg * STAGE;
-    const uint8_t* sB = sA + BM * 128;
+    const uint8_t* sB = sA + BM * RB;
 #pragma unroll
     for (int s = 0; s < BK / 16; ++s) {
       const int c = 2 * s + fk;
       half8 bf[FN], af[FM];
 #pragma unroll
-      for (int i = 0; i < FN; ++i) bf[i] = *reinterpret_cast<const half8*>(sB + swz(wn * TN + i * 32 + fr, c));
+      for (int i = 0; i < FN; ++i) bf[i] = *reinterpret_cast<const half8*>(sB + swz<BK>(wn * TN + i * 32 + fr, c));
 #pragma unroll
-      for (int j = 0; j < FM; ++j) af[j] = *reinterpret_cast<const half8*>(sA + swz(wm * TM + j * 32 + fr, c));
+      for (int j = 0; j < FM; ++j) af[j] = *reinterpret_cast<const half8*>(sA + swz<BK>(wm * TM + j * 32 + fr, c));
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -131,90 +186,151 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
     }
   };
 
+  // LDS stage kt % 2 holds k tile kt; register set r holds the tile with index
+  // congruent to r mod PF. At step kt the free set (kt % PF) starts loading tile
+  // kt + PF, so each tile's loads have PF compute phases to land.
   const int KT = (K + BK - 1) / BK;
-  gload(0);
-  lstore(0);
+#pragma unroll
+  for (int p = 0; p < PF; ++p)
+    if (p < KT) gload(ra[p], rb[p], p);
+  lstore(ra[0], rb[0], 0);
   __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt + 1 < KT) gload(kt + 1);
-    compute(kt & 1);
-    if (kt + 1 < KT) lstore((kt + 1) & 1);
-    __syncthreads();
+  int kt0 = 0;
+  // Steady state: every step of the group issues its loads unconditionally, so
+  // the compiler's wait counts can let the younger register sets stay in flight.
+  for (; kt0 + 2 * PF - 1 < KT; kt0 += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      gload(ra[u], rb[u], kt0 + u + PF);
+      compute((kt0 + u) & 1);
+      lstore(ra[(u + 1) % PF], rb[(u + 1) % PF], (kt0 + u + 1) & 1);
+      __syncthreads();
+    }
   }
-
-  // ---- epilogue: (acc * sa[m]) * sb[n] + bias[n] -> bf16, 8-byte runs ----
+  // Tail: the last < 2 * PF tiles, with guarded loads.
+  for (; kt0 < KT; kt0 += PF) {
 #pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int m = m0 + wm * TM + j * 32 + fr;
-    if (m >= M) continue;
-    float sa;
-    if constexpr (A_BF16) sa = ldexp1(-a_exp[m]);
-    else sa = a_sinv[m];
-    uint16_t* crow = C + (int64_t)m * ldc;
-#pragma unroll
-    for (int i = 0; i < FN; ++i) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * TN + i * 32 + 8 * q + 4 * fk;
-        if (n >= N) continue;
-        const float4 sb = *reinterpret_cast<const float4*>(b_sinv + n);
-        float bb[4] = {0.f, 0.f, 0.f, 0.f};
-        if (bias) {
-          const uint32_t b01 = *reinterpret_cast<const uint32_t*>(bias + n);
-          const uint32_t b23 = *reinterpret_cast<const uint32_t*>(bias + n + 2);
-          bb[0] = bf16_lo(b01); bb[1] = bf16_hi(b01); bb[2] = bf16_lo(b23); bb[3] = bf16_hi(b23);
-        }
-        const float y0 = fmaf(acc[i][j][4 * q + 0] * sa, sb.x, bb[0]);
-        const float y1 = fmaf(acc[i][j][4 * q + 1] * sa, sb.y, bb[1]);
-        const float y2 = fmaf(acc[i][j][4 * q + 2] * sa, sb.z, bb[2]);
-        const float y3 = fmaf(acc[i][j][4 * q + 3] * sa, sb.w, bb[3]);
-        *reinterpret_cast<uint2*>(crow + n) = make_uint2(pack_bf16(y0, y1), pack_bf16(y2, y3));
+    for (int u = 0; u < PF; ++u) {
+      const int kt = kt0 + u;
+      if (kt < KT) {
+        if (kt + PF < KT) gload(ra[u], rb[u], kt + PF);
+        compute(kt & 1);
+        if (kt + 1 < KT) lstore(ra[(u + 1) % PF], rb[(u + 1) % PF], (kt + 1) & 1);
+        __syncthreads();
       }
     }
+  }
+
+  // ---- epilogue: (acc * sa[m]) * sb[n] + bias[n] -> bf16, staged through LDS so
+  // that each row of the tile leaves as whole 16-byte-per-lane runs ----
+#pragma unroll
+  for (int pass = 0; pass < PASSES; ++pass) {
+    if (wm * TM / RPP == pass) {
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int ml = wm * TM + j * 32 + fr;  // row within the tile
+        const int m = m0 + ml;
+        float sa = 0.f;
+        if (EVEN || m < M) {
+          if constexpr (A_BF16) sa = ldexp1(-a_exp[m]);
+          else sa = a_sinv[m];
+        }
+        uint8_t* srow = smem + (ml - pass * RPP) * PITCH;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int nl = wn * TN + i * 32 + 8 * q + 4 * fk;
+            const int n = n0 + nl;
+            float4 sb = make_float4(0.f, 0.f, 0.f, 0.f);
+            float bb[4] = {0.f, 0.f, 0.f, 0.f};
+            if (EVEN || n < N) {
+              sb = *reinterpret_cast<const float4*>(b_sinv + n);
+              if (bias) {
+                const uint32_t b01 = *reinterpret_cast<const uint32_t*>(bias + n);
+                const uint32_t b23 = *reinterpret_cast<const uint32_t*>(bias + n + 2);
+                bb[0] = bf16_lo(b01); bb[1] = bf16_hi(b01); bb[2] = bf16_lo(b23); bb[3] = bf16_hi(b23);
+              }
+            }
+            const float y0 = fmaf(acc[i][j][4 * q + 0] * sa, sb.x, bb[0]);
+            const float y1 = fmaf(acc[i][j][4 * q + 1] * sa, sb.y, bb[1]);
+            const float y2 = fmaf(acc[i][j][4 * q + 2] * sa, sb.z, bb[2]);
+            const float y3 = fmaf(acc[i][j][4 * q + 3] * sa, sb.w, bb[3]);
+            *reinterpret_cast<uint2*>(srow + nl * 2) = make_uint2(pack_bf16(y0, y1), pack_bf16(y2, y3));
+          }
+        }
+      }
+    }
+    __syncthreads();
+    constexpr int OCR = BN / 8;  // 16-byte chunks per output tile row
+#pragma unroll
+    for (int c = tid; c < RPP * OCR; c += NT) {
+      const int rl = c / OCR, cc = c % OCR;
+      const int m = m0 + pass * RPP + rl, n = n0 + cc * 8;
+      if (EVEN || (m < M && n < N))
+        stg16(C + (int64_t)m * ldc + n, *reinterpret_cast<const uint4*>(smem + rl * PITCH + cc * 16));
+    }
+    if (PASSES > 1) __syncthreads();
   }
 }
 
 struct TileCfg {
-  int bm, bn;
+  int bm, bn, bk;
 };
-constexpr TileCfg kCfgs[] = {{256, 256}, {128, 128}, {64, 64}, {64, 32}};
-constexpr int kNumCfgs = 4;
+// 0: 256x256, 8 waves of 64x128 (2 waves/SIMD), k tile 32, prefetch 2
+// 1: 128x128, 4 waves of 64x64, k tile 64, prefetch 2
+// 2: 64x64, 4 waves of 32x32, k tile 64, prefetch 2
+// 3: 64x32, 1 wave, k tile 64, prefetch 2 (skinny M)
+// 4: 256x256, 8 waves of 64x128, k tile 64, prefetch 1
+// 5: 256x256, 8 waves of 64x128, k tile 32, prefetch 3
+// 6: 256x256, 4 waves of 128x128 (1 wave/SIMD), k tile 32, prefetch 2
+constexpr TileCfg kCfgs[] = {{256, 256, 32}, {128, 128, 64}, {64, 64, 64}, {64, 32, 64},
+                             {256, 256, 64}, {256, 256, 32}, {256, 256, 32}};
+constexpr int kNumCfgs = 7;
 
 int pick_cfg(int64_t M, int64_t N) {
   auto tiles = [&](int c) { return cdiv(M, kCfgs[c].bm) * cdiv(N, kCfgs[c].bn); };
-  if (tiles(0) >= 192) return 0;
-  if (tiles(1) >= 160) return 1;
-  if (M <= 64) return 3;
+  if (tiles(5) >= 128) return 5;  // 256x256, k tile 32, prefetch 3
+  if (tiles(1) >= 256) return 1;
   return 2;
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int PF, bool A_BF16>
+void launch_cfg(bool even, unsigned blocks, const uint16_t* a, int64_t lda, const int32_t* a_exp, const float* a_sinv,
+                const uint16_t* b, int64_t ldb, const float* b_sinv, const uint16_t* bi, uint16_t* c, int64_t ldc,
+                int M, int N, int K, hipStream_t st) {
+  if (even)
+    gemm_kernel<BM, BN, WM, WN, BK, PF, A_BF16, true><<<blocks, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
+                                                                               bi, c, ldc, M, N, K);
+  else
+    gemm_kernel<BM, BN, WM, WN, BK, PF, A_BF16, false><<<blocks, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
+                                                                                bi, c, ldc, M, N, K);
 }
 
 template <bool A_BF16>
 int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const float* a_sinv, const void* B,
                 int64_t ldb, const float* b_sinv, const void* bias, void* C, int64_t ldc, int64_t M, int64_t N,
                 int64_t K, hipStream_t st) {
-  const int64_t blocks = cdiv(M, kCfgs[cfg].bm) * cdiv(N, kCfgs[cfg].bn);
+  const int bm = kCfgs[cfg].bm, bn = kCfgs[cfg].bn;
+  const int64_t blocks = cdiv(M, bm) * cdiv(N, bn);
   TB_CHECK(blocks < (int64_t)1 << 31, "gemm: grid too large");
+  const bool even = M % bm == 0 && N % bn == 0 && K % kCfgs[cfg].bk == 0;
   const auto a = (const uint16_t*)A;
   const auto b = (const uint16_t*)B;
   const auto bi = (const uint16_t*)bias;
   const auto c = (uint16_t*)C;
+  const unsigned g = (unsigned)blocks;
   switch (cfg) {
-    case 0:
-      gemm_kernel<256, 256, 4, 2, A_BF16><<<(unsigned)blocks, 512, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c,
-                                                                            ldc, (int)M, (int)N, (int)K);
-      break;
-    case 1:
-      gemm_kernel<128, 128, 2, 2, A_BF16><<<(unsigned)blocks, 256, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c,
-                                                                            ldc, (int)M, (int)N, (int)K);
-      break;
-    case 2:
-      gemm_kernel<64, 64, 2, 2, A_BF16><<<(unsigned)blocks, 256, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c,
-                                                                          ldc, (int)M, (int)N, (int)K);
-      break;
-    default:
-      gemm_kernel<64, 32, 1, 1, A_BF16><<<(unsigned)blocks, 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c,
-                                                                         ldc, (int)M, (int)N, (int)K);
-      break;
+#define CFG(BM_, BN_, WM_, WN_, BK_, PF_) \
+  launch_cfg<BM_, BN_, WM_, WN_, BK_, PF_, A_BF16>(even, g, a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, ldc, M, N, K, st)
+    case 0: CFG(256, 256, 4, 2, 32, 2); break;
+    case 1: CFG(128, 128, 2, 2, 64, 2); break;
+    case 2: CFG(64, 64, 2, 2, 64, 2); break;
+    case 3: CFG(64, 32, 1, 1, 64, 2); break;
+    case 4: CFG(256, 256, 4, 2, 64, 1); break;
+    case 5: CFG(256, 256, 4, 2, 32, 3); break;
+    default: CFG(256, 256, 2, 2, 32, 2); break;
+#undef CFG
   }
   TB_LAUNCH_CHECK("gemm");
   return 0;
@@ -229,6 +345,8 @@ int check_gemm(const char* fn, int64_t M, int64_t N, int64_t K, const void* A, i
            "%s: row strides must be multiples of 8", fn);
   TB_CHECK(aligned16(A) && aligned16(B) && aligned16(C) && aligned16(sb), "%s: operands must be 16-byte aligned", fn);
   TB_CHECK(bias == nullptr || aligned4(bias), "%s: bias must be 4-byte aligned", fn);
+  // tile row offsets are 32-bit byte offsets from the tile's first row
+  TB_CHECK(lda < (int64_t)1 << 22 && ldb < (int64_t)1 << 22, "%s: row stride too large", fn);
   return 0;
 }
 
