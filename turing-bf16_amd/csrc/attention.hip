@@ -19,6 +19,8 @@
 //  - output bf16(O / l * 2^ev) written from registers: one rounding.
 // Causal blocks are launched heaviest first; key tiles past the diagonal are
 // skipped, only tiles crossing it are masked.
+#include <stdlib.h>
+
 #include <algorithm>
 #include <math.h>
 
@@ -35,7 +37,7 @@ int launch_head_amax_partial(const void* x, int dtype, int64_t B, int64_t H, int
 
 namespace {
 
-constexpr int BQ = 128, BKV = 64, NTH = 256;
+constexpr int BKV = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct FwdParams {
@@ -67,25 +69,30 @@ __device__ __forceinline__ int swz_k(int row, int chunk) {
 
 __device__ __forceinline__ int swz_vt(int d, int chunk) { return d * 128 + ((chunk ^ ((d >> 1) & 7)) << 4); }
 
-// Block-wide max of an int (256 threads).
+// Block-wide max of an int (NT threads, one slot per wave in red).
+template <int NT>
 __device__ __forceinline__ int block_max_int(int v, int* red) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
-  return max(max(red[0], red[1]), max(red[2], red[3]));
+  int r = red[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) r = max(r, red[i]);
+  return r;
 }
 
 // max over heads of frexp(max over chunks of partial[bh][c])
+template <int NT>
 __device__ int heads_max_exp(const float* part, int nbh, int nch, int* red) {
   int e = INT_MIN;
-  for (int bh = threadIdx.x; bh < nbh; bh += NTH) {
+  for (int bh = threadIdx.x; bh < nbh; bh += NT) {
     float m = 0.f;
     for (int c = 0; c < nch; ++c) m = fmaxf(m, part[bh * nch + c]);
     e = max(e, frexp_exp(m));
   }
-  return block_max_int(e, red);
+  return block_max_int<NT>(e, red);
 }
 
 __device__ __forceinline__ int head_exp_of(const float* part, int bh, int nch) {
@@ -94,30 +101,49 @@ __device__ __forceinline__ int head_exp_of(const float* part, int bh, int nch) {
   return frexp_exp(m);
 }
 
-template <int DP, bool CAUSAL, bool HAS_BIAS>
-__global__ __launch_bounds__(NTH) void attn_fwd_kernel(FwdParams p) {
+// Halves j of four rows (packed fp16 words w0..w3 holding halves 2i, 2i+1) -> the
+// 4-key run {r0[j], r1[j], r2[j], r3[j]} as two dwords, with v_perm_b32.
+__device__ __forceinline__ uint2 gather4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, bool odd) {
+  const uint32_t sel = odd ? 0x07060302u : 0x05040100u;
+  return make_uint2(__builtin_amdgcn_perm(w1, w0, sel), __builtin_amdgcn_perm(w3, w2, sel));
+}
+
+// Forward kernel: NW waves, 32 query rows each (BQ = 32 * NW), 64-key tiles.
+// NW = 8 (two waves per SIMD, K/V conversion shared by 256 queries): waves 0-3
+// stage K, waves 4-7 stage V^T. NW = 4: every thread stages both. PF register
+// sets of prefetched K/V tiles.
+template <int DP, int NW, int PF, bool CAUSAL, bool HAS_BIAS>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(DP > 128 ? 1 : 2, DP > 128 ? 1 : 2))) void
+attn_fwd_kernel(FwdParams p) {
+  constexpr int NT = NW * 64, BQW = 32 * NW;
   constexpr int KS = DP / 16;            // MFMA k-steps over the head dim
   constexpr int DB = DP / 32;            // 32-wide d blocks of O^T
   constexpr int CPR = DP / 8;            // 16-byte chunks per K row
-  constexpr int KROWS = NTH / CPR;       // K rows per load pass
-  constexpr int KL = BKV / KROWS;        // K loads per thread
-  constexpr int VBLK = 16 * (DP / 8);    // 4-key x 8-d blocks in a V tile
-  constexpr int VL = (VBLK + NTH - 1) / NTH;
+  constexpr int KTH = NW == 8 ? NT / 2 : NT;  // threads staging K
+  constexpr int VTH = NW == 8 ? NT / 2 : NT;  // threads staging V
+  constexpr int VT0 = NW == 8 ? NT / 2 : 0;   // first V-staging thread
+  constexpr int KL = BKV * CPR / KTH;         // K chunks per staging thread
+  constexpr int VBLK = 16 * CPR;              // 4-key x 8-d blocks in a V tile
+  constexpr int VL = (VBLK + VTH - 1) / VTH;  // V blocks per staging thread
+  static_assert(KL * KTH == BKV * CPR, "K staging");
+  // one staging array shared by the K and V roles: [K chunks][V blocks x 4 rows]
+  constexpr int VOFF = NW == 8 ? 0 : KL;
+  constexpr int SL = NW == 8 ? (KL > 4 * VL ? KL : 4 * VL) : KL + 4 * VL;
   constexpr int KBYTES = BKV * DP * 2;
   constexpr int STAGE = KBYTES + DP * 128;
   __shared__ __align__(16) uint8_t smem[2 * STAGE];
-  __shared__ int red[4];
+  __shared__ int red[NW];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, fk = lane >> 5;
   const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
   const int hk = h / (p.H / p.Hkv);
   const int qt = CAUSAL ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;
-  const int q0 = qt * BQ;
+  const int q0 = qt * BQW;
 
   // ---- exponents ----
-  const int eq = heads_max_exp(p.part_q, p.B * p.H, p.nch_q, red);
-  const int ek = heads_max_exp(p.part_k, p.B * p.Hkv, p.nch_k, red);
+  const int eq = heads_max_exp<NT>(p.part_q, p.B * p.H, p.nch_q, red);
+  const int ek = heads_max_exp<NT>(p.part_k, p.B * p.Hkv, p.nch_k, red);
   int a = (ek - eq) >> 1;  // floor division
   a = max(min(a, 14 - eq), ek - 14);
   const int ev = head_exp_of(p.part_v, b * p.Hkv + hk, p.nch_v) - p.v_exp;
@@ -126,7 +152,7 @@ __global__ __launch_bounds__(NTH) void attn_fwd_kernel(FwdParams p) {
       p.exps[0] = a;
       p.exps[1] = 0;
     }
-    for (int i = tid; i < p.B * p.Hkv; i += NTH) p.exps[2 + i] = head_exp_of(p.part_v, i, p.nch_v) - p.v_exp;
+    for (int i = tid; i < p.B * p.Hkv; i += NT) p.exps[2 + i] = head_exp_of(p.part_v, i, p.nch_v) - p.v_exp;
   }
   const float sq = ldexp1(a), sk = ldexp1(-a), sv = ldexp1(-ev);
 
@@ -144,61 +170,68 @@ __global__ __launch_bounds__(NTH) void attn_fwd_kernel(FwdParams p) {
     }
   }
 
-  // ---- K / V staging ----
-  const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-  const uint16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
-  uint4 rk[KL];
-  uint4 rv[VL][4];
-  auto gload = [&](int kb) {
-    const int key0 = kb * BKV;
+  // ---- K / V staging through buffer loads (rows past Sk load as zeros) ----
+  const BufRes kres = make_res(p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh,
+                               min<int64_t>((int64_t)p.Sk * p.k_ss * 2, 0x7fffffff));
+  const BufRes vres = make_res(p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh,
+                               min<int64_t>((int64_t)p.Sk * p.v_ss * 2, 0x7fffffff));
+  const bool k_stager = NW != 8 || tid < KTH;
+  const bool v_stager = NW != 8 || tid >= VT0;
+  const int ktid = NW == 8 ? tid : tid, vtid = tid - VT0;
+  uint4 st[PF][SL];
+  auto gload = [&](uint4(&sr)[SL], int kb) {
+    const int soff_k = kb * BKV * (int)p.k_ss * 2, soff_v = kb * BKV * (int)p.v_ss * 2;
+    if (k_stager) {
 #pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int row = tid / CPR + i * KROWS, c = tid % CPR;
-      const int key = key0 + row, d = c * 8;
-      rk[i] = (key < p.Sk && d < p.D) ? ldg16(kbase + (int64_t)key * p.k_ss + d) : make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < KL; ++i) {
+        const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
+        const uint4 v = buf_load16(kres, (row * (int)p.k_ss + ch * 8) * 2, soff_k);
+        sr[i] = ch * 8 < p.D ? v : make_uint4(0, 0, 0, 0);
+      }
     }
+    if (v_stager) {
 #pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int blk = tid + i * NTH;
-      const int kg = blk & 15, dc = blk >> 4;
-      const int d = dc * 8;
+      for (int i = 0; i < VL; ++i) {
+        const int blk = vtid + i * VTH;
+        const int kg = blk & 15, dc = blk >> 4;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = key0 + 4 * kg + r;
-        rv[i][r] = (blk < VBLK && key < p.Sk && d < p.D) ? ldg16(vbase + (int64_t)key * p.v_ss + d)
-                                                        : make_uint4(0, 0, 0, 0);
+        for (int r = 0; r < 4; ++r) {
+          const uint4 v = buf_load16(vres, ((4 * kg + r) * (int)p.v_ss + dc * 8) * 2, soff_v);
+          sr[VOFF + 4 * i + r] = (blk < VBLK && dc * 8 < p.D) ? v : make_uint4(0, 0, 0, 0);
+        }
       }
     }
   };
-  auto lstore = [&](int stg) {
+  auto lstore = [&](const uint4(&sr)[SL], int stg) {
     uint8_t* sK = smem + stg * STAGE;
     uint8_t* sV = sK + KBYTES;
+    if (k_stager) {
 #pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int row = tid / CPR + i * KROWS, c = tid % CPR;
-      *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, c)) = cvt_bf16x8_f16x8(rk[i], sk);
+      for (int i = 0; i < KL; ++i) {
+        const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
+        *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, ch)) = cvt_bf16x8_f16x8(sr[i], sk);
+      }
     }
+    if (v_stager) {
 #pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int blk = tid + i * NTH;
-      if (blk >= VBLK) continue;
-      const int kg = blk & 15, dc = blk >> 4;
-      uint4 cv[4];
+      for (int i = 0; i < VL; ++i) {
+        const int blk = vtid + i * VTH;
+        if (blk >= VBLK) continue;
+        const int kg = blk & 15, dc = blk >> 4;
+        uint4 cv[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) cv[r] = cvt_bf16x8_f16x8(rv[i][r], sv);
-      const int pos = perm16(4 * kg);  // 4 consecutive keys stay consecutive
-      const int chunk = pos >> 3, half_off = (pos & 7) * 2;
-      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
-      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
-      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&cv[2]);
-      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
+        for (int r = 0; r < 4; ++r) cv[r] = cvt_bf16x8_f16x8(sr[VOFF + 4 * i + r], sv);
+        const int pos = perm16(4 * kg);  // 4 consecutive keys stay consecutive
+        const int chunk = pos >> 3, half_off = (pos & 7) * 2;
+        const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
+        const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
+        const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&cv[2]);
+        const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int sh = (j & 1) * 16;
-        const uint32_t e0 = (w0[j >> 1] >> sh) & 0xffffu, e1 = (w1[j >> 1] >> sh) & 0xffffu;
-        const uint32_t e2 = (w2[j >> 1] >> sh) & 0xffffu, e3 = (w3[j >> 1] >> sh) & 0xffffu;
-        const int d = dc * 8 + j;
-        *reinterpret_cast<uint2*>(sV + swz_vt(d, chunk) + half_off) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+        for (int j = 0; j < 8; ++j) {
+          const uint2 g = gather4(w0[j >> 1], w1[j >> 1], w2[j >> 1], w3[j >> 1], j & 1);
+          *reinterpret_cast<uint2*>(sV + swz_vt(dc * 8 + j, chunk) + half_off) = g;
+        }
       }
     }
   };
@@ -208,27 +241,22 @@ __global__ __launch_bounds__(NTH) void attn_fwd_kernel(FwdParams p) {
   for (int i = 0; i < DB; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_o[i][r] = 0.f;
+  // running max in log2 units; stays stale until a row's max grows by more than
+  // 2^8, so exp2 arguments are <= 8 and P <= 256 (fp16-safe)
   float m_run = -INFINITY, l_run = 0.f;
+  const float c = HAS_BIAS ? 1.f : p.scale_log2;
 
   const int nkb_all = (p.Sk + BKV - 1) / BKV;
   int nkb = nkb_all;
-  if constexpr (CAUSAL) nkb = min(nkb_all, (min(q0 + BQ, p.Sq) + BKV - 1) / BKV);
+  if constexpr (CAUSAL) nkb = min(nkb_all, (min(q0 + BQW, p.Sq) + BKV - 1) / BKV);
   const uint16_t* brow = nullptr;
   if constexpr (HAS_BIAS)
     brow = p.bias + (int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh + (int64_t)min(qrow, p.Sq - 1) * p.bias_sq;
 
-  if (nkb > 0) {
-    gload(0);
-    lstore(0);
-  }
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int stg = kb & 1;
-    if (kb + 1 < nkb) gload(kb + 1);
-    const uint8_t* sK = smem + stg * STAGE;
+  auto step = [&](int kb) {
+    const uint8_t* sK = smem + (kb & 1) * STAGE;
     const uint8_t* sV = sK + KBYTES;
-
-    // S^T = K Q^T for two 32-key halves
+    // S^T = K Q^T for two 32-key halves: lane = one query row, 16 keys each
     floatx16 sacc[2];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
@@ -240,46 +268,46 @@ __global__ __launch_bounds__(NTH) void attn_fwd_kernel(FwdParams p) {
         sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[kh], 0, 0, 0);
       }
     }
-
-    // logits in log2 units, masking, running max
     const int key0 = kb * BKV;
-    const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0);
+    const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0 + wave * 32);
     float mx = -INFINITY;
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
+        float sv_ = sacc[kh][r];
         const int key = key0 + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-        float s = sacc[kh][r] * p.scale_log2;
         if constexpr (HAS_BIAS) {
-          if (key < p.Sk) s += (float)__builtin_bit_cast(_Float16, brow[key]) * kLog2e;
+          sv_ = sv_ * p.scale_log2 + (key < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[key]) * kLog2e : 0.f);
         }
-        if (edge && (key >= p.Sk || (CAUSAL && key > qrow))) s = -INFINITY;
-        sacc[kh][r] = s;
-        mx = fmaxf(mx, s);
+        if (edge && (key >= p.Sk || (CAUSAL && key > qrow))) sv_ = -INFINITY;
+        sacc[kh][r] = sv_;
+        mx = fmaxf(mx, sv_);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+    if (__any(mx > m_run + 8.f)) {  // wave-uniform: rescale O and l only when some row needs it
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
+    }
+    const float mneg = (m_run == -INFINITY) ? 0.f : -m_run;
     float lsum = 0.f;
     uint32_t pk[2][8];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(sacc[kh][r] - m_use);
-        const float p1 = __builtin_amdgcn_exp2f(sacc[kh][r + 1] - m_use);
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r], c, mneg));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r + 1], c, mneg));
         lsum += p0 + p1;
         pk[kh][r >> 1] = pack_f16(p0, p1);
       }
-    l_run = l_run * alpha + lsum;
-#pragma unroll
-    for (int i = 0; i < DB; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
-
+    l_run += lsum;
     // O^T += V^T P^T over four 16-key steps
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -292,9 +320,37 @@ __global__ __launch_bounds__(NTH) void attn_fwd_kernel(FwdParams p) {
         acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc_o[db], 0, 0, 0);
       }
     }
+  };
 
-    if (kb + 1 < nkb) lstore(stg ^ 1);
-    __syncthreads();
+  // Pipeline as in the GEMM: LDS stage kb % 2 holds tile kb, register set u holds
+  // the tile congruent to u mod PF; the steady state issues its loads
+  // unconditionally so the younger sets stay in flight.
+#pragma unroll
+  for (int i = 0; i < PF; ++i)
+    if (i < nkb) gload(st[i], i);
+  if (nkb > 0) lstore(st[0], 0);
+  __syncthreads();
+  int kb0 = 0;
+  for (; kb0 + 2 * PF - 1 < nkb; kb0 += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      gload(st[u], kb0 + u + PF);
+      step(kb0 + u);
+      lstore(st[(u + 1) % PF], (kb0 + u + 1) & 1);
+      __syncthreads();
+    }
+  }
+  for (; kb0 < nkb; kb0 += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int kb = kb0 + u;
+      if (kb < nkb) {
+        if (kb + PF < nkb) gload(st[u], kb + PF);
+        step(kb);
+        if (kb + 1 < nkb) lstore(st[(u + 1) % PF], (kb + 1) & 1);
+        __syncthreads();
+      }
+    }
   }
 
   // ---- epilogue ----
@@ -315,9 +371,9 @@ __global__ __launch_bounds__(NTH) void attn_fwd_kernel(FwdParams p) {
           make_uint2(pack_bf16(y[0] * sev, y[1] * sev), pack_bf16(y[2] * sev, y[3] * sev));
       if (p.o16) *reinterpret_cast<uint2*>(p.o16 + orow + d) = make_uint2(pack_f16(y[0], y[1]), pack_f16(y[2], y[3]));
     }
+  // lse in log2 units (v_log_f32); rows that see no key get +inf so the
+  // backward's exp2(logit - lse) is 0 there
   if (p.lse && fk == 0)
-    // log2(l) via v_log_f32; rows that see no key get +inf so the backward's
-    // exp2(logit - lse) is 0 there
     p.lse[(int64_t)bh * p.Sq + qrow] = (l_tot > 0.f) ? m_run + __builtin_amdgcn_logf(l_tot) : INFINITY;
 }
 
@@ -338,17 +394,32 @@ WsLayout fwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk) {
   return w;
 }
 
-template <int DP>
-int launch_fwd_dp(const FwdParams& p, bool causal, bool has_bias, dim3 grid, hipStream_t st) {
+template <int DP, int NW, int PF>
+int launch_fwd_nw(const FwdParams& p, bool causal, bool has_bias, dim3 grid, hipStream_t st) {
+  // masked variants keep one register set: the bias reads need the registers
   if (causal) {
-    if (has_bias) attn_fwd_kernel<DP, true, true><<<grid, NTH, 0, st>>>(p);
-    else attn_fwd_kernel<DP, true, false><<<grid, NTH, 0, st>>>(p);
+    if (has_bias) attn_fwd_kernel<DP, NW, 1, true, true><<<grid, NW * 64, 0, st>>>(p);
+    else attn_fwd_kernel<DP, NW, PF, true, false><<<grid, NW * 64, 0, st>>>(p);
   } else {
-    if (has_bias) attn_fwd_kernel<DP, false, true><<<grid, NTH, 0, st>>>(p);
-    else attn_fwd_kernel<DP, false, false><<<grid, NTH, 0, st>>>(p);
+    if (has_bias) attn_fwd_kernel<DP, NW, 1, false, true><<<grid, NW * 64, 0, st>>>(p);
+    else attn_fwd_kernel<DP, NW, PF, false, false><<<grid, NW * 64, 0, st>>>(p);
   }
   TB_LAUNCH_CHECK("attn_fwd");
   return 0;
+}
+
+// 8-wave blocks (256 queries) share each converted K/V tile between more queries;
+// they are used when there are enough of them to balance the causal triangle.
+// Head dim 256 always uses 4-wave blocks (one wave per SIMD, 512 registers).
+template <int DP>
+int launch_fwd_dp(const FwdParams& p, bool causal, bool has_bias, hipStream_t st, int nw_override) {
+  const int64_t tiles8 = cdiv(p.Sq, 256) * p.B * p.H;
+  int nw = nw_override > 0 ? nw_override : (tiles8 >= 512 ? 8 : 4);
+  if (DP > 128) nw = 4;
+  if (nw == 8) {
+    if constexpr (DP <= 128) return launch_fwd_nw<DP, 8, 2>(p, causal, has_bias, dim3((unsigned)cdiv(p.Sq, 256), p.B * p.H), st);
+  }
+  return launch_fwd_nw<DP, 4, 1>(p, causal, has_bias, dim3((unsigned)cdiv(p.Sq, 128), p.B * p.H), st);
 }
 
 int check_bhsd(const char* fn, const char* name, const void* x, const int64_t* st, int64_t D) {
@@ -417,8 +488,9 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   p.lse = lse;
   p.o16 = (uint16_t*)o16;
   p.exps = exps;
-  dim3 grid((unsigned)cdiv(Sq, BQ), (unsigned)(B * H));
-  if (D <= 64) return launch_fwd_dp<64>(p, causal != 0, bias != nullptr, grid, st);
-  if (D <= 128) return launch_fwd_dp<128>(p, causal != 0, bias != nullptr, grid, st);
-  return launch_fwd_dp<256>(p, causal != 0, bias != nullptr, grid, st);
+  const char* ov = getenv("TBF16_ATTN_WAVES");  // benchmarking override: 4 or 8
+  const int nw = ov ? atoi(ov) : 0;
+  if (D <= 64) return launch_fwd_dp<64>(p, causal != 0, bias != nullptr, st, nw);
+  if (D <= 128) return launch_fwd_dp<128>(p, causal != 0, bias != nullptr, st, nw);
+  return launch_fwd_dp<256>(p, causal != 0, bias != nullptr, st, nw);
 }

@@ -44,35 +44,6 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   else return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
-typedef int int4v __attribute__((ext_vector_type(4)));
-
-// The raw buffer load intrinsic with a 4 x i32 resource (this form keeps the
-// descriptor in SGPRs; the pointer-typed builtin lost uniformity through the
-// staging lambdas and produced a waterfall loop around every load).
-__device__ int4v raw_buffer_load_b128(int4v rsrc, int voffset, int soffset, int aux) __asm(
-    "llvm.amdgcn.raw.buffer.load.v4i32");
-
-// Raw buffer resource over [p, p + bytes): loads past the end return zeros.
-// Dword 3 = 0x00020000 is the gfx9-family raw-buffer format word.
-struct BufRes {
-  int lo, hi, bytes;
-};
-__device__ __forceinline__ BufRes make_res(const void* p, int64_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(p);
-  return BufRes{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes};
-}
-// 16-byte buffer load; the descriptor is rebuilt from scalars at the use so the
-// compiler keeps it in SGPRs (a descriptor it cannot prove uniform costs a
-// waterfall loop per load and breaks its wait-count tracking).
-__device__ __forceinline__ uint4 buf_load16(BufRes r, int voffset, int soffset) {
-  int4v d;
-  d.x = __builtin_amdgcn_readfirstlane(r.lo);
-  d.y = __builtin_amdgcn_readfirstlane(r.hi);
-  d.z = __builtin_amdgcn_readfirstlane(r.bytes);
-  d.w = 0x00020000;
-  return __builtin_bit_cast(uint4, raw_buffer_load_b128(d, voffset, __builtin_amdgcn_readfirstlane(soffset), 0));
-}
-
 template <int BM, int BN, int WM, int WN, int BK, int PF, bool A_BF16, bool EVEN>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                            const int32_t* __restrict__ a_exp,
