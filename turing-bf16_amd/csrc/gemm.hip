@@ -7,17 +7,19 @@
 // b is fp16 (prepare_weight's w16) with fp32 inverse row scales sb.
 //
 // Tiling (gfx950, 64-wide waves, 160 KB LDS):
-//  - block tile BM (rows of a) x BN (rows of b), k tile 64; WM x WN waves, each
-//    owning a (BM/WM) x (BN/WN) sub-tile made of 32x32 MFMA blocks
+//  - block tile BM (rows of a) x BN (rows of b), k tile BK (32 or 64); WM x WN
+//    waves, each owning a (BM/WM) x (BN/WN) sub-tile made of 32x32 MFMA blocks
 //    (v_mfma_f32_32x32x16_f16: 16 fp32 accumulators per lane per block).
-//  - operands staged global -> VGPR -> LDS with 16-byte loads, two LDS stages and
-//    the next k tile's loads in flight during the current tile's MFMAs; one
-//    barrier per k tile. LDS rows are 128 bytes (64 fp16) with the 16-byte chunk
-//    index XOR-swizzled by (row / 2) % 8, so the 32-row fragment reads
-//    (ds_read_b128) and the 8-lanes-per-row stores are bank-conflict free.
-//  - two register sets alternate (loop unrolled by two), so each k tile's global
-//    loads are issued two compute phases before they are needed; tiles that are
-//    full in M, N and K use unpredicated loads.
+//  - operands staged global -> VGPR -> LDS with 16-byte buffer loads. LDS rows
+//    are BK fp16 with the 16-byte chunk index XOR-swizzled, so the 32-row
+//    fragment reads (ds_read_b128) and the row stores are bank-conflict free.
+//  - PF register sets are in flight: each k tile's global loads are issued PF
+//    compute phases before they are stored to LDS.
+//  - the headline shape uses three LDS stages in a ring with fragments read
+//    one 16-wide k step ahead of the MFMAs (the next tile's first step
+//    included), one barrier per k tile, and an instruction-group schedule that
+//    spreads a k step's LDS reads, A conversions, LDS writes and global loads
+//    between its MFMAs; the two-stage form is kept for the smaller tiles.
 //  - the MFMA's first operand is the b fragment, the second the a fragment, so a
 //    lane's 16 accumulators are four runs of 4 consecutive n for one m. The
 //    epilogue rounds once to bf16, stages the tile rows in LDS and writes each
@@ -25,7 +27,10 @@
 //    written back in partial sectors, ~5x the output bytes).
 //  - block ids are remapped so that each XCD (8 per chip, round-robin dispatch)
 //    gets a contiguous range of tiles, grouped 8 a-tiles deep for L2 reuse.
+// M <= 64 (decode) uses a separate skinny kernel that splits K across waves
+// (see skinny_kernel below).
 #include <algorithm>
+#include <type_traits>
 
 #include "abi_util.h"
 #include "common.h"
@@ -44,7 +49,7 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   else return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int PF, bool A_BF16, bool EVEN>
+template <int BM, int BN, int WM, int WN, int BK, int PF, int NS, bool A_BF16, bool EVEN>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                            const int32_t* __restrict__ a_exp,
                                                            const float* __restrict__ a_sinv,
@@ -66,7 +71,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   constexpr int PFIT = (BM * PITCH <= 2 * STAGE) ? 1 : (BM / 2 * PITCH <= 2 * STAGE) ? 2 : 4;
   constexpr int PASSES = PFIT < BM / TM ? PFIT : BM / TM;
   constexpr int RPP = BM / PASSES;
-  constexpr int SMEM = 2 * STAGE > RPP * PITCH ? 2 * STAGE : RPP * PITCH;
+  constexpr int NSTG = NS >= 3 ? 3 : 2;  // LDS stages
+  constexpr bool SCHED = NS == 4;
+  constexpr int SMEM = NSTG * STAGE > RPP * PITCH ? NSTG * STAGE : RPP * PITCH;
   __shared__ __align__(16) uint8_t smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -157,37 +164,131 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
     }
   };
 
-  // LDS stage kt % 2 holds k tile kt; register set r holds the tile with index
-  // congruent to r mod PF. At step kt the free set (kt % PF) starts loading tile
-  // kt + PF, so each tile's loads have PF compute phases to land.
   const int KT = (K + BK - 1) / BK;
-#pragma unroll
-  for (int p = 0; p < PF; ++p)
-    if (p < KT) gload(ra[p], rb[p], p);
-  lstore(ra[0], rb[0], 0);
-  __syncthreads();
-  int kt0 = 0;
-  // Steady state: every step of the group issues its loads unconditionally, so
-  // the compiler's wait counts can let the younger register sets stay in flight.
-  for (; kt0 + 2 * PF - 1 < KT; kt0 += PF) {
-#pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      gload(ra[u], rb[u], kt0 + u + PF);
-      compute((kt0 + u) & 1);
-      lstore(ra[(u + 1) % PF], rb[(u + 1) % PF], (kt0 + u + 1) & 1);
-      __syncthreads();
-    }
-  }
-  // Tail: the last < 2 * PF tiles, with guarded loads.
-  for (; kt0 < KT; kt0 += PF) {
-#pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int kt = kt0 + u;
-      if (kt < KT) {
-        if (kt + PF < KT) gload(ra[u], rb[u], kt + PF);
-        compute(kt & 1);
-        if (kt + 1 < KT) lstore(ra[(u + 1) % PF], rb[(u + 1) % PF], (kt + 1) & 1);
+  if constexpr (NS == 2) {
+    // LDS stage kt % 2 holds k tile kt; register set r holds the tile with index
+    // congruent to r mod PF. At step kt the free set (kt % PF) starts loading tile
+    // kt + PF, so each tile's loads have PF compute phases to land.
+  #pragma unroll
+    for (int p = 0; p < PF; ++p)
+      if (p < KT) gload(ra[p], rb[p], p);
+    lstore(ra[0], rb[0], 0);
+    __syncthreads();
+    int kt0 = 0;
+    // Steady state: every step of the group issues its loads unconditionally, so
+    // the compiler's wait counts can let the younger register sets stay in flight.
+    for (; kt0 + 2 * PF - 1 < KT; kt0 += PF) {
+  #pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        gload(ra[u], rb[u], kt0 + u + PF);
+        compute((kt0 + u) & 1);
+        lstore(ra[(u + 1) % PF], rb[(u + 1) % PF], (kt0 + u + 1) & 1);
         __syncthreads();
+      }
+    }
+    // Tail: the last < 2 * PF tiles, with guarded loads.
+    for (; kt0 < KT; kt0 += PF) {
+  #pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int kt = kt0 + u;
+        if (kt < KT) {
+          if (kt + PF < KT) gload(ra[u], rb[u], kt + PF);
+          compute(kt & 1);
+          if (kt + 1 < KT) lstore(ra[(u + 1) % PF], rb[(u + 1) % PF], (kt + 1) & 1);
+          __syncthreads();
+        }
+      }
+    }
+  } else {
+    // Three LDS stages in a ring (tile kt in stage kt % 3) and fragments read one
+    // 16-wide k step ahead of the MFMAs that use them, the next tile's first step
+    // included: an MFMA never waits on the LDS read issued just before it. In step
+    // kt a wave stores tile kt + 2 (stage (kt + 2) % 3 = (kt - 1) % 3, whose last
+    // reads finished before the previous barrier) and starts the global loads of
+    // tile kt + 2 + PF into the register set just emptied; one barrier per tile
+    // publishes tile kt + 2 and retires the reads of stage kt % 3.
+    constexpr int SUB = BK / 16;
+    static_assert(SUB % 2 == 0, "fragment double buffer needs an even number of k steps");
+    half8 fb[2][FN], fa[2][FM];
+    auto fread = [&](half8(&bf)[FN], half8(&af)[FM], int stg, int s) {
+      const uint8_t* sA = smem + stg * STAGE;
+      const uint8_t* sB = sA + BM * RB;
+      const int c = 2 * s + fk;
+#pragma unroll
+      for (int i = 0; i < FN; ++i) bf[i] = *reinterpret_cast<const half8*>(sB + swz<BK>(wn * TN + i * 32 + fr, c));
+#pragma unroll
+      for (int j = 0; j < FM; ++j) af[j] = *reinterpret_cast<const half8*>(sA + swz<BK>(wm * TM + j * 32 + fr, c));
+    };
+    auto mma = [&](const half8(&bf)[FN], const half8(&af)[FM]) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[i], af[j], acc[i][j], 0, 0, 0);
+    };
+    // one k tile; LOAD/STORE/NEXT say whether tile kt + 2 + PF is loaded, tile
+    // kt + 2 stored and tile kt + 1's first fragments read (guarded in the tail)
+    // Optional instruction-group schedule (NS == 4): each MFMA of a k step is
+    // followed by its share of the step's LDS reads, A conversions, LDS writes and
+    // global loads, so a wave keeps the matrix pipe fed while it does them.
+    constexpr int MF = FN * FM, RD = FN + FM, WR = AL + BL, LD = AL + BL;
+    constexpr int VT = A_BF16 ? 20 * AL : 0;  // VALU ops of one tile's A conversion
+    auto sched = [&](bool staging) {
+      if constexpr (SCHED) {
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          if (i < RD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+          if (staging) {
+            if (VT) __builtin_amdgcn_sched_group_barrier(0x002, (VT + MF - 1) / MF, 0);  // VALU
+            if (i >= MF - WR) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+            if (i >= MF - LD) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    auto tile = [&](int kt, int stg, int u, bool store, bool load, bool next) {
+      const int stg1 = stg == 2 ? 0 : stg + 1, stg2 = stg1 == 2 ? 0 : stg1 + 1;
+#pragma unroll
+      for (int s = 0; s < SUB; ++s) {
+        if (s + 1 < SUB) fread(fb[(s + 1) & 1], fa[(s + 1) & 1], stg, s + 1);
+        else if (next) fread(fb[0], fa[0], stg1, 0);
+        if (s == 0) {
+          if (store) lstore(ra[u], rb[u], stg2);
+          if (load) gload(ra[u], rb[u], kt + 2 + PF);
+        }
+        mma(fb[s & 1], fa[s & 1]);
+        sched(s == 0);
+      }
+      __syncthreads();
+    };
+    // prologue: tiles 0 and 1 stored, tiles 2 .. PF + 1 in flight (set j % PF)
+    static_assert(PF >= 2, "three-stage ring needs two register sets");
+#pragma unroll
+    for (int q = 0; q < PF; ++q)
+      if (q < KT) gload(ra[q], rb[q], q);
+    lstore(ra[0], rb[0], 0);
+    if (PF < KT) gload(ra[0], rb[0], PF);
+    if (KT > 1) lstore(ra[1], rb[1], 1);
+    if (PF + 1 < KT) gload(ra[1], rb[1], PF + 1);
+    __syncthreads();
+    fread(fb[0], fa[0], 0, 0);
+    int kt0 = 0, stg = 0;
+    for (; kt0 + 2 + PF + PF - 1 < KT; kt0 += PF) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        tile(kt0 + u, stg, (u + 2) % PF, true, true, true);
+        stg = stg == 2 ? 0 : stg + 1;
+      }
+    }
+    for (; kt0 < KT; kt0 += PF) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int kt = kt0 + u;
+        if (kt < KT) {
+          tile(kt, stg, (u + 2) % PF, kt + 2 < KT, kt + 2 + PF < KT, kt + 1 < KT);
+          stg = stg == 2 ? 0 : stg + 1;
+        }
       }
     }
   }
@@ -245,36 +346,240 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   }
 }
 
-struct TileCfg {
-  int bm, bn, bk;
-};
-// 0: 256x256, 8 waves of 64x128 (2 waves/SIMD), k tile 32, prefetch 2
-// 1: 128x128, 4 waves of 64x64, k tile 64, prefetch 2
-// 2: 64x64, 4 waves of 32x32, k tile 64, prefetch 2
-// 3: 64x32, 1 wave, k tile 64, prefetch 2 (skinny M)
-// 4: 256x256, 8 waves of 64x128, k tile 64, prefetch 1
-// 5: 256x256, 8 waves of 64x128, k tile 32, prefetch 3
-// 6: 256x256, 4 waves of 128x128 (1 wave/SIMD), k tile 32, prefetch 2
-constexpr TileCfg kCfgs[] = {{256, 256, 32}, {128, 128, 64}, {64, 64, 64}, {64, 32, 64},
-                             {256, 256, 64}, {256, 256, 32}, {256, 256, 32}};
-constexpr int kNumCfgs = 7;
+// Skinny GEMM for M <= 32 * MB rows of a (decode and small batches). One block
+// per 32 * NB rows of b; its NW waves split K into interleaved 64-wide chunks
+// (wave w takes chunks w, w + NW, ...). Each operand value is used by a single
+// wave, so both go global -> registers -> MFMA with no LDS staging: a lane loads
+// 64 contiguous bytes of one row per chunk, and lane half h of MFMA k step j
+// holds k = 32 h + 8 j + [0, 8) of the chunk for both operands (the same k-slot
+// assignment on both sides gives the same dot products). PF chunks per wave are
+// in flight. The NW partial tiles are summed through LDS in the epilogue and
+// rounded once to bf16.
+template <int NB, int MB, int NW, int PF, bool TR, bool A_BF16>
+__global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                         const int32_t* __restrict__ a_exp,
+                                                         const float* __restrict__ a_sinv,
+                                                         const uint16_t* __restrict__ B, int64_t ldb,
+                                                         const float* __restrict__ b_sinv,
+                                                         const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
+                                                         int64_t ldc, int M, int N, int K) {
+  constexpr int NT = NW * 64, NBLK = NB * MB;
+  constexpr int RED = NW * NBLK * 16 * 64 * 4, TSLOT = NB * 32 * 128;  // TR: one chunk of b rows per wave
+  constexpr int SMEM = TR && NW * TSLOT > RED ? NW * TSLOT : RED;
+  __shared__ __align__(16) uint8_t smem[SMEM];
+  float* red = reinterpret_cast<float*>(smem);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int n0 = blockIdx.x * 32 * NB;
+  uint8_t* tslot = smem + wave * TSLOT;
 
+  // rows past N (M) lie past the resources' ends and load as zeros; pieces past
+  // K are zeroed by a select
+  const BufRes bres = make_res(B + (int64_t)n0 * ldb, min<int64_t>((int64_t)(N - n0) * ldb * 2, 0x7fffffff));
+  const BufRes ares = make_res(A, min<int64_t>((int64_t)M * lda * 2, 0x7fffffff));
+  int boff[NB], aoff[MB];
+  float as[MB];
+  // TR: b is loaded coalesced (load q of block nb: rows 32 nb + 8 q + lane / 8,
+  // 16-byte chunk lane % 8 of the chunk's 128-byte row piece) and transposed
+  // into MFMA fragments through a per-wave LDS slot, the chunk index
+  // XOR-swizzled by (row / 2) % 8 so that both sides are bank-conflict free.
+  // Otherwise lane (r, h) loads 64 contiguous bytes of row r directly.
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) boff[nb] = ((32 * nb + fr) * (int)ldb + 32 * fh) * 2;
+  int toff[NB][4];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) toff[nb][q] = ((32 * nb + 8 * q + (lane >> 3)) * (int)ldb + 8 * (lane & 7)) * 2;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = 32 * mb + fr;
+    aoff[mb] = (m * (int)lda + 32 * fh) * 2;
+    if constexpr (A_BF16) as[mb] = m < M ? pow2f(a_exp[m]) : 0.f;
+  }
+  const int KC = (K + 63) / 64;
+  const int NI = wave < KC ? (KC - 1 - wave) / NW + 1 : 0;  // chunks of this wave
+
+  uint4 wr[PF][NB][4], xr[PF][MB][4];
+  // chunk i of this wave into a register set; only a wave's last chunk can run
+  // past K, so the steady state loads without the zeroing select (a select
+  // right after the load makes the compiler wait for the load there)
+  auto gload = [&](uint4(&w)[NB][4], uint4(&x)[MB][4], int i, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    const int c = wave + i * NW;
+    const int soff = c * 128;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool ok = !MASKED || c * 64 + 32 * fh + 8 * q < K;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if constexpr (TR) {
+          // zero pieces past K (the piece's k is 8 * (lane % 8) of the chunk)
+          const uint4 v = buf_load16(bres, toff[nb][q], soff);
+          w[nb][q] = !MASKED || c * 64 + 8 * (lane & 7) < K ? v : make_uint4(0, 0, 0, 0);
+        } else {
+          const uint4 v = buf_load16(bres, boff[nb] + 16 * q, soff);
+          w[nb][q] = ok ? v : make_uint4(0, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const uint4 v = buf_load16(ares, aoff[mb] + 16 * q, soff);
+        x[mb][q] = ok ? v : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  floatx16 acc[NB][MB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[nb][mb][r] = 0.f;
+  auto compute = [&](const uint4(&w)[NB][4], const uint4(&x)[MB][4]) {
+    uint4 wt[NB][4];
+    if constexpr (TR) {
+      // through LDS: same wave, so program order keeps the previous chunk's reads
+      // ahead of these writes
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = 32 * nb + 8 * q + (lane >> 3);
+          *reinterpret_cast<uint4*>(tslot + row * 128 + (((lane & 7) ^ ((row >> 1) & 7)) << 4)) = w[nb][q];
+        }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = 32 * nb + fr;
+          wt[nb][j] = *reinterpret_cast<const uint4*>(tslot + row * 128 + (((4 * fh + j) ^ ((row >> 1) & 7)) << 4));
+        }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wt[nb][j] = w[nb][j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      half8 xf[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        xf[mb] = __builtin_bit_cast(half8, A_BF16 ? cvt_bf16x8_f16x8(x[mb][j], as[mb]) : x[mb][j]);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          acc[nb][mb] =
+              __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, wt[nb][j]), xf[mb], acc[nb][mb], 0, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < PF; ++u)
+    if (u < NI) gload(wr[u], xr[u], u, std::true_type{});
+  int i0 = 0;
+  // Steady state: unconditional loads, and scheduling barriers between the
+  // steps so that the compiler keeps each step's loads after its MFMAs (left
+  // free, it hoists the next chunks' loads, reuses their registers early and
+  // ends up waiting for loads it has just issued).
+  for (; i0 + 2 * PF - 1 < NI; i0 += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      compute(wr[u], xr[u]);
+      __builtin_amdgcn_sched_barrier(0);
+      gload(wr[u], xr[u], i0 + u + PF, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  for (; i0 < NI; i0 += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      if (i0 + u < NI) {
+        compute(wr[u], xr[u]);
+        if (i0 + u + PF < NI) gload(wr[u], xr[u], i0 + u + PF, std::true_type{});
+      }
+    }
+  }
+
+  // ---- sum the NW partial tiles, scale, round once to bf16 ----
+  if constexpr (TR) __syncthreads();  // the transpose slots alias red
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((wave * NBLK + nb * MB + mb) * 16 + r) * 64 + lane] = acc[nb][mb][r];
+  __syncthreads();
+  for (int g = tid; g < NBLK * 4 * 64; g += NT) {
+    const int blk = g >> 8, rq = (g >> 6) & 3, ln = g & 63;
+    const int nb = blk / MB, mb = blk % MB;
+    const int m = 32 * mb + (ln & 31), n = n0 + 32 * nb + 8 * rq + 4 * (ln >> 5);
+    if (m >= M || n >= N) continue;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += red[((w * NBLK + blk) * 16 + 4 * rq + e) * 64 + ln];
+    float sa;
+    if constexpr (A_BF16) sa = ldexp1(-a_exp[m]);
+    else sa = a_sinv[m];
+    const float4 sb = *reinterpret_cast<const float4*>(b_sinv + n);
+    float bb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (bias) {
+      const uint32_t b01 = *reinterpret_cast<const uint32_t*>(bias + n);
+      const uint32_t b23 = *reinterpret_cast<const uint32_t*>(bias + n + 2);
+      bb[0] = bf16_lo(b01); bb[1] = bf16_hi(b01); bb[2] = bf16_lo(b23); bb[3] = bf16_hi(b23);
+    }
+    const float y0 = fmaf(v[0] * sa, sb.x, bb[0]), y1 = fmaf(v[1] * sa, sb.y, bb[1]);
+    const float y2 = fmaf(v[2] * sa, sb.z, bb[2]), y3 = fmaf(v[3] * sa, sb.w, bb[3]);
+    *reinterpret_cast<uint2*>(C + (int64_t)m * ldc + n) = make_uint2(pack_bf16(y0, y1), pack_bf16(y2, y3));
+  }
+}
+
+struct TileCfg {
+  int bm, bn, bk;  // skinny configurations: bm = the largest M they take
+  bool skinny;
+};
+// Tiled configurations (block tile, waves, k tile, register sets in flight, LDS stages):
+// 0: 256x256, 8 waves of 64x128 (2 per SIMD), k 32, 3 sets, 3 stages, grouped MFMA schedule
+// 1: 128x128, 4 waves of 64x64, k 64, 2 sets, 2 stages
+// 2: 64x64, 4 waves of 32x32, k 64, 2 sets, 2 stages
+// 3: 128x128, 4 waves of 64x64, k 64, 2 sets, 3 stages
+// 4: 256x256, 8 waves of 64x128, k 32, 3 sets, 2 stages (no grouped schedule)
+// Skinny configurations (M <= bm; 4 waves splitting K; block = 32 NB rows of b):
+// 5: M <= 32, b registers-direct, 4 chunks in flight
+// 6: M <= 32, b loaded coalesced and transposed through LDS, 4 chunks in flight
+// 7: M <= 64, as 6 with 3 chunks in flight
+// 8: M <= 64, 64 b rows per block, as 6 with 2 chunks in flight
+constexpr TileCfg kCfgs[] = {{256, 256, 32}, {128, 128, 64}, {64, 64, 64},       {128, 128, 64},    {256, 256, 32},
+                             {32, 32, 64, true}, {32, 32, 64, true}, {64, 32, 64, true}, {64, 64, 64, true}};
+constexpr int kNumCfgs = 9;
+
+// Measured on MI355X (4096^3; 8192x6144x2048; decode K = 2560, N = 10240):
+// the grouped-schedule 256x256 tile wherever it fills the chip, the 64-row
+// skinny block for M <= 64 when there are enough b rows to keep 160 blocks busy.
 int pick_cfg(int64_t M, int64_t N) {
   auto tiles = [&](int c) { return cdiv(M, kCfgs[c].bm) * cdiv(N, kCfgs[c].bn); };
-  if (tiles(5) >= 128) return 5;  // 256x256, k tile 32, prefetch 3
+  if (M <= 64) {
+    if (cdiv(N, 64) >= 160) return 8;
+    return M <= 32 ? 6 : 7;
+  }
+  if (tiles(0) >= 128) return 0;
   if (tiles(1) >= 256) return 1;
+  if (tiles(3) >= 128) return 3;
   return 2;
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int PF, bool A_BF16>
+template <int BM, int BN, int WM, int WN, int BK, int PF, int NS, bool A_BF16>
 void launch_cfg(bool even, unsigned blocks, const uint16_t* a, int64_t lda, const int32_t* a_exp, const float* a_sinv,
                 const uint16_t* b, int64_t ldb, const float* b_sinv, const uint16_t* bi, uint16_t* c, int64_t ldc,
                 int M, int N, int K, hipStream_t st) {
   if (even)
-    gemm_kernel<BM, BN, WM, WN, BK, PF, A_BF16, true><<<blocks, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
+    gemm_kernel<BM, BN, WM, WN, BK, PF, NS, A_BF16, true><<<blocks, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
                                                                                bi, c, ldc, M, N, K);
   else
-    gemm_kernel<BM, BN, WM, WN, BK, PF, A_BF16, false><<<blocks, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
+    gemm_kernel<BM, BN, WM, WN, BK, PF, NS, A_BF16, false><<<blocks, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
                                                                                 bi, c, ldc, M, N, K);
 }
 
@@ -283,7 +588,8 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
                 int64_t ldb, const float* b_sinv, const void* bias, void* C, int64_t ldc, int64_t M, int64_t N,
                 int64_t K, hipStream_t st) {
   const int bm = kCfgs[cfg].bm, bn = kCfgs[cfg].bn;
-  const int64_t blocks = cdiv(M, bm) * cdiv(N, bn);
+  TB_CHECK(!kCfgs[cfg].skinny || M <= bm, "gemm: configuration %d takes M <= %d", cfg, bm);
+  const int64_t blocks = kCfgs[cfg].skinny ? cdiv(N, bn) : cdiv(M, bm) * cdiv(N, bn);
   TB_CHECK(blocks < (int64_t)1 << 31, "gemm: grid too large");
   const bool even = M % bm == 0 && N % bn == 0 && K % kCfgs[cfg].bk == 0;
   const auto a = (const uint16_t*)A;
@@ -292,15 +598,21 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
   const auto c = (uint16_t*)C;
   const unsigned g = (unsigned)blocks;
   switch (cfg) {
-#define CFG(BM_, BN_, WM_, WN_, BK_, PF_) \
-  launch_cfg<BM_, BN_, WM_, WN_, BK_, PF_, A_BF16>(even, g, a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, ldc, M, N, K, st)
-    case 0: CFG(256, 256, 4, 2, 32, 2); break;
-    case 1: CFG(128, 128, 2, 2, 64, 2); break;
-    case 2: CFG(64, 64, 2, 2, 64, 2); break;
-    case 3: CFG(64, 32, 1, 1, 64, 2); break;
-    case 4: CFG(256, 256, 4, 2, 64, 1); break;
-    case 5: CFG(256, 256, 4, 2, 32, 3); break;
-    default: CFG(256, 256, 2, 2, 32, 2); break;
+#define CFG(BM_, BN_, WM_, WN_, BK_, PF_, NS_) \
+  launch_cfg<BM_, BN_, WM_, WN_, BK_, PF_, NS_, A_BF16>(even, g, a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, ldc, M, N, K, st)
+    case 0: CFG(256, 256, 4, 2, 32, 3, 4); break;
+    case 1: CFG(128, 128, 2, 2, 64, 2, 2); break;
+    case 2: CFG(64, 64, 2, 2, 64, 2, 2); break;
+    case 3: CFG(128, 128, 2, 2, 64, 2, 3); break;
+    case 4: CFG(256, 256, 4, 2, 32, 3, 2); break;
+#define SKINNY(NB_, MB_, NW_, PF_, TR_)                                                                         \
+  skinny_kernel<NB_, MB_, NW_, PF_, TR_, A_BF16><<<g, NW_ * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, \
+                                                                        ldc, M, N, K)
+    case 5: SKINNY(1, 1, 4, 4, false); break;
+    case 6: SKINNY(1, 1, 4, 4, true); break;
+    case 7: SKINNY(1, 2, 4, 3, true); break;
+    default: SKINNY(2, 2, 4, 2, true); break;
+#undef SKINNY
 #undef CFG
   }
   TB_LAUNCH_CHECK("gemm");

@@ -95,6 +95,28 @@ def call(name: str, *args) -> None:
         raise RuntimeError(f"tbf16: {msg}")
 
 
+_raw_stream = torch._C._cuda_getCurrentRawStream
+
+
+def launch(name: str, where, *args) -> None:
+    """Calls entry point `name` with `args` followed by torch's current stream on the
+    device of `where` (a tensor or a torch.device). Every launching entry point takes
+    its stream last. The device guard is entered only when that device is not the
+    current one, which keeps a decode-sized call's host cost to a few microseconds."""
+    fn = getattr(lib(), name)
+    dev = where.get_device() if isinstance(where, torch.Tensor) else where.index
+    if dev is None or dev < 0:
+        raise ValueError("tbf16: expected tensors on a ROCm (cuda) device")
+    if torch.cuda.current_device() != dev:
+        with torch.cuda.device(dev):
+            rc = fn(*args, _raw_stream(dev))
+    else:
+        rc = fn(*args, _raw_stream(dev))
+    if rc != 0:
+        msg = lib().tbf16_last_error().decode(errors="replace")
+        raise RuntimeError(f"tbf16: {msg}")
+
+
 def ptr(t) -> int | None:
     """Device pointer of a tensor (None for None)."""
     return None if t is None else t.data_ptr()

@@ -18,7 +18,7 @@ import weakref
 import torch
 import torch.nn.functional as F
 
-from ._ext import available, call, ptr  # noqa: F401  (available re-exported as in the reference)
+from ._ext import available, launch, ptr  # noqa: F401  (available re-exported as in the reference)
 
 # TBF16_GEMM=fused forces the max-scaled fused path for every M >= 2 (the reference's
 # switch between its fused kernel and the cuBLAS path, tbf16/ops.py:31-33). Unset:
@@ -40,10 +40,6 @@ def _target_exp(K: int) -> int:
     K * 4^t, which must stay under fp16's 65504; t = 0 covers K <= 32768
     (tbf16/ops.py:40-43)."""
     return min(0, (15 - math.ceil(math.log2(max(K, 1)))) // 2)
-
-
-def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def _dev_check(*ts):
@@ -81,9 +77,8 @@ def quantize_rows(x: torch.Tensor, target_exp: int = 0, l1: bool = False):
     y = torch.empty((R, Kp), device=x.device, dtype=torch.float16)
     s_inv = torch.empty((R,), device=x.device, dtype=torch.float32)
     if R:
-        with torch.cuda.device(x.device):
-            call("tbf16_quantize_rows", ptr(xk), R, Kp, xk.stride(0), int(target_exp), int(l1), ptr(y), y.stride(0),
-                 ptr(s_inv), _stream(x))
+        launch("tbf16_quantize_rows", x, ptr(xk), R, Kp, xk.stride(0), int(target_exp), int(l1), ptr(y), y.stride(0),
+               ptr(s_inv))
     return (y if Kp == K else y[:, :K]), s_inv
 
 
@@ -158,13 +153,11 @@ def _linear(x2, w16, w_sinv, bias, t, l1):
     M, Kp = x2.shape
     y = torch.empty((M, Np), device=x2.device, dtype=torch.bfloat16)
     exps = torch.empty((M,), device=x2.device, dtype=torch.int32)
-    with torch.cuda.device(x2.device):
-        call("tbf16_linear", ptr(x2), M, Kp, x2.stride(0), ptr(w16), Np, w16.stride(0), ptr(ws), ptr(b), ptr(y),
-             y.stride(0), int(t), int(l1), _GEMM_CFG, ptr(exps), _stream(x2))
+    launch("tbf16_linear", x2, ptr(x2), M, Kp, x2.stride(0), ptr(w16), Np, w16.stride(0), ptr(ws), ptr(b), ptr(y),
+           y.stride(0), int(t), int(l1), _GEMM_CFG, ptr(exps))
     return y if Np == N else y[:, :N]
 
 
-@torch.autocast("cuda", enabled=False)
 def scaled_linear(x: torch.Tensor, w16: torch.Tensor, w_sinv: torch.Tensor, bias=None):
     """y = x @ W^T + b for bf16 x, with W given by prepare_weight. Returns bf16
     (tbf16/ops.py:164-175). M < 2 -> GEMV; M >= FUSED_MIN_M -> one fused kernel with
@@ -184,7 +177,6 @@ def scaled_linear(x: torch.Tensor, w16: torch.Tensor, w_sinv: torch.Tensor, bias
     return _linear(x2, w16, w_sinv, bias, t, l1).reshape(*shape[:-1], N)
 
 
-@torch.autocast("cuda", enabled=False)
 def linear_q(x16, x_sinv, w16, w_sinv, bias=None):
     """GEMM + epilogue on already-quantized rows: (x16 * x_sinv) @ (w16 * w_sinv)^T + bias,
     bf16 (M, N) (tbf16/ops.py:178-189). fp32 accumulation, one bf16 rounding (the
@@ -195,9 +187,8 @@ def linear_q(x16, x_sinv, w16, w_sinv, bias=None):
     sa = x_sinv.float().contiguous()
     y = torch.empty((M, Np), device=x16.device, dtype=torch.bfloat16)
     if M:
-        with torch.cuda.device(x16.device):
-            call("tbf16_gemm_f16", ptr(x16), M, x16.shape[1], x16.stride(0), ptr(sa), ptr(w16), Np, w16.stride(0),
-                 ptr(ws), ptr(b), ptr(y), y.stride(0), _GEMM_CFG, _stream(x16))
+        launch("tbf16_gemm_f16", x16, ptr(x16), M, x16.shape[1], x16.stride(0), ptr(sa), ptr(w16), Np, w16.stride(0),
+               ptr(ws), ptr(b), ptr(y), y.stride(0), _GEMM_CFG)
     return y if Np == N else y[:, :N]
 
 
@@ -213,6 +204,5 @@ def small_m_linear(x2: torch.Tensor, w16: torch.Tensor, w_sinv: torch.Tensor, bi
     ws = w_sinv.float().contiguous()
     b = _bias_bf16(bias, N, x2.device)
     y = torch.empty((1, N), device=x2.device, dtype=torch.bfloat16)
-    with torch.cuda.device(x2.device):
-        call("tbf16_gemv", ptr(xk), ptr(wk), N, wk.shape[1], wk.stride(0), ptr(ws), ptr(b), ptr(y), _stream(x2))
+    launch("tbf16_gemv", x2, ptr(xk), ptr(wk), N, wk.shape[1], wk.stride(0), ptr(ws), ptr(b), ptr(y))
     return y
