@@ -123,46 +123,6 @@ __device__ __forceinline__ uint4 buf_load16(BufRes r, int voffset, int soffset) 
   return __builtin_bit_cast(uint4, raw_buffer_load_b128(d, voffset, __builtin_amdgcn_readfirstlane(soffset), 0));
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// 16-byte buffer load straight into LDS (gfx950): lane l's bytes land at
-// lds + 16 * l, so a wave fills 1 KB; lds must be the same for the whole wave.
-// Written as inline asm on purpose: the compiler makes every LDS read that
-// follows the intrinsic form (or an asm statement with a memory clobber) wait
-// for all such loads, since it cannot tell ring slots apart, and that
-// serialises a prefetch pipeline. Here the compiler does not see the LDS write,
-// so callers order it themselves:
-//  - vm_wait<n>() before reading a slot (loads complete in issue order);
-//  - `after` is a value produced by the last LDS read of the slot's previous
-//    contents: it goes through v_readfirstlane (which the compiler makes wait
-//    for that read) into an operand of the asm, so the load is not issued
-//    before the read has returned. (An unused VGPR operand of an asm statement
-//    is not enough: the compiler does not wait for it.)
-// The compiler's own vmcnt waits for other loads stay correct: they count only
-// the loads it knows of, so they wait for at least as much as they need.
-__device__ __forceinline__ void buf_load_lds16(BufRes r, void* lds, int voffset, int soffset, uint32_t after) {
-  int4v d;
-  d.x = __builtin_amdgcn_readfirstlane(r.lo);
-  d.y = __builtin_amdgcn_readfirstlane(r.hi);
-  d.z = __builtin_amdgcn_readfirstlane(r.bytes);
-  d.w = 0x00020000;
-  const int m0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(lds_void*)lds);
-  const int dep = __builtin_amdgcn_readfirstlane((int)after);
-  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :
-               : "v"(voffset), "s"(d), "s"(__builtin_amdgcn_readfirstlane(soffset)), "s"(m0), "s"(dep)
-               : "m0");
-}
-
-// s_waitcnt vmcnt(n) alone (expcnt and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-
-
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void stg16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 
