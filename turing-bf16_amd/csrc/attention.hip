@@ -7,7 +7,7 @@
 // q, k, v are read as bf16 and converted on the fly: q16 = q * 2^a, k16 = k * 2^-a,
 // v16 = v * 2^-ev (exact powers of two), so no scaled copies exist in HBM.
 //
-// Block = 4 waves, 128 query rows (32 per wave); key tiles of 64.
+// Block = 4 or 8 waves, 32 query rows per wave; key tiles of 64.
 //  - a wave keeps its 32 q rows as MFMA fragments in registers for the whole
 //    kernel and computes S^T = K Q^T with v_mfma_f32_32x32x16_f16 (K from LDS), so
 //    each lane owns ONE query row: row max / sum need one exchange with lane ^ 32.
@@ -16,9 +16,12 @@
 //    each 16-key group by swapping index bits 2 and 3) so that the A fragment of
 //    a lane is one 16-byte read and P's fragment comes straight from S^T's
 //    accumulators without any cross-lane shuffle.
+//  - row sums l come from the fp16 P that enters the PV product (v_dot2 with
+//    ones), so the normalisation matches the weights actually applied.
 //  - output bf16(O / l * 2^ev) written from registers: one rounding.
 // Causal blocks are launched heaviest first; key tiles past the diagonal are
-// skipped, only tiles crossing it are masked.
+// skipped, and only tiles crossing the diagonal or the end of the keys take the
+// (wave-uniform) masking branch.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -99,6 +102,19 @@ __device__ __forceinline__ int head_exp_of(const float* part, int bh, int nch) {
   float m = 0.f;
   for (int c = 0; c < nch; ++c) m = fmaxf(m, part[bh * nch + c]);
   return frexp_exp(m);
+}
+
+// Masks the scores of a key tile that crosses the end of the keys or (causal)
+// the diagonal: keys >= Sk or > qmax become -inf. Lane layout of S^T: key
+// key0 + 32 kh + 8 (r / 4) + 4 fk + r % 4 in accumulator r of half kh. Called
+// from a wave-uniform branch, so interior tiles skip it.
+__device__ __forceinline__ void mask_tile(floatx16 (&sacc)[2], int key0, int Sk, int qmax, int fk) {
+  const int lim = min(Sk - 1, qmax) - key0 - 4 * fk;  // keep offsets <= lim
+#pragma unroll
+  for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (kh * 32 + 8 * (r >> 2) + (r & 3) > lim) sacc[kh][r] = -INFINITY;
 }
 
 // Halves j of four rows (packed fp16 words w0..w3 holding halves 2i, 2i+1) -> the
@@ -185,8 +201,7 @@ attn_fwd_kernel(FwdParams p) {
 #pragma unroll
       for (int i = 0; i < KL; ++i) {
         const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
-        const uint4 v = buf_load16(kres, (row * (int)p.k_ss + ch * 8) * 2, soff_k);
-        sr[i] = ch * 8 < p.D ? v : make_uint4(0, 0, 0, 0);
+        sr[i] = buf_load16(kres, (row * (int)p.k_ss + ch * 8) * 2, soff_k);
       }
     }
     if (v_stager) {
@@ -196,8 +211,8 @@ attn_fwd_kernel(FwdParams p) {
         const int kg = blk & 15, dc = blk >> 4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint4 v = buf_load16(vres, ((4 * kg + r) * (int)p.v_ss + dc * 8) * 2, soff_v);
-          sr[VOFF + 4 * i + r] = (blk < VBLK && dc * 8 < p.D) ? v : make_uint4(0, 0, 0, 0);
+          // d >= D rows of V^T only feed O^T rows that are never written: no zeroing
+          sr[VOFF + 4 * i + r] = buf_load16(vres, ((4 * kg + r) * (int)p.v_ss + dc * 8) * 2, soff_v);
         }
       }
     }
@@ -206,10 +221,15 @@ attn_fwd_kernel(FwdParams p) {
     uint8_t* sK = smem + stg * STAGE;
     uint8_t* sV = sK + KBYTES;
     if (k_stager) {
+      // K columns d >= D (the next row's values when D < DP) meet zero Q columns,
+      // but must be zero themselves so that no inf or nan there reaches S
+      const bool kpad = p.D < DP;
 #pragma unroll
       for (int i = 0; i < KL; ++i) {
         const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
-        *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, ch)) = cvt_bf16x8_f16x8(sr[i], sk);
+        uint4 v = sr[i];
+        if (kpad) v = ch * 8 < p.D ? v : make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, ch)) = cvt_bf16x8_f16x8(v, sk);
       }
     }
     if (v_stager) {
@@ -270,20 +290,22 @@ attn_fwd_kernel(FwdParams p) {
     }
     const int key0 = kb * BKV;
     const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0 + wave * 32);
+    if constexpr (HAS_BIAS) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = key0 + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+          sacc[kh][r] = sacc[kh][r] * p.scale_log2 +
+                        (key < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[key]) * kLog2e : 0.f);
+        }
+    }
+    if (edge) mask_tile(sacc, key0, p.Sk, CAUSAL ? qrow : INT_MAX, fk);
     float mx = -INFINITY;
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float sv_ = sacc[kh][r];
-        const int key = key0 + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-        if constexpr (HAS_BIAS) {
-          sv_ = sv_ * p.scale_log2 + (key < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[key]) * kLog2e : 0.f);
-        }
-        if (edge && (key >= p.Sk || (CAUSAL && key > qrow))) sv_ = -INFINITY;
-        sacc[kh][r] = sv_;
-        mx = fmaxf(mx, sv_);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kh][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
     if (__any(mx > m_run + 8.f)) {  // wave-uniform: rescale O and l only when some row needs it
       const float m_new = fmaxf(m_run, mx);
@@ -296,6 +318,8 @@ attn_fwd_kernel(FwdParams p) {
         for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
     }
     const float mneg = (m_run == -INFINITY) ? 0.f : -m_run;
+    // row sums from the fp16 P that the PV product uses (v_dot2 with ones)
+    const half2v ones = {(_Float16)1.f, (_Float16)1.f};
     float lsum = 0.f;
     uint32_t pk[2][8];
 #pragma unroll
@@ -304,8 +328,8 @@ attn_fwd_kernel(FwdParams p) {
       for (int r = 0; r < 16; r += 2) {
         const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r], c, mneg));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r + 1], c, mneg));
-        lsum += p0 + p1;
         pk[kh][r >> 1] = pack_f16(p0, p1);
+        lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pk[kh][r >> 1]), ones, lsum, false);
       }
     l_run += lsum;
     // O^T += V^T P^T over four 16-key steps
@@ -409,12 +433,15 @@ int launch_fwd_nw(const FwdParams& p, bool causal, bool has_bias, dim3 grid, hip
 }
 
 // 8-wave blocks (256 queries) share each converted K/V tile between more queries;
-// they are used when there are enough of them to balance the causal triangle.
-// Head dim 256 always uses 4-wave blocks (one wave per SIMD, 512 registers).
+// 4-wave blocks (128 queries, two blocks per CU) overlap better on their own,
+// since the two co-resident blocks run out of phase. Measured on MI355X (causal,
+// B = 1, H = 16, D = 128): 8 waves win at S = 4096 (256 blocks), 4 waves at
+// S = 16384 (1024 blocks). Head dim 256 always uses 4-wave blocks (one wave per
+// SIMD, 512 registers).
 template <int DP>
 int launch_fwd_dp(const FwdParams& p, bool causal, bool has_bias, hipStream_t st, int nw_override) {
   const int64_t tiles8 = cdiv(p.Sq, 256) * p.B * p.H;
-  int nw = nw_override > 0 ? nw_override : (tiles8 >= 512 ? 8 : 4);
+  int nw = nw_override > 0 ? nw_override : (tiles8 >= 128 && tiles8 < 1024 ? 8 : 4);
   if (DP > 128) nw = 4;
   if (nw == 8) {
     if constexpr (DP <= 128) return launch_fwd_nw<DP, 8, 2>(p, causal, has_bias, dim3((unsigned)cdiv(p.Sq, 256), p.B * p.H), st);
