@@ -149,10 +149,10 @@ __device__ __forceinline__ void store_blk_both(uint8_t* sRow, uint8_t* sT, const
   const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int sh = (j & 1) * 16;
-    const uint32_t e0 = (w0[j >> 1] >> sh) & 0xffffu, e1 = (w1[j >> 1] >> sh) & 0xffffu;
-    const uint32_t e2 = (w2[j >> 1] >> sh) & 0xffffu, e3 = (w3[j >> 1] >> sh) & 0xffffu;
-    *reinterpret_cast<uint2*>(sT + swz_t(dc * 8 + j, chunk) + hoff) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+    // halves j of the four rows -> one 4-element run, two v_perm_b32
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    *reinterpret_cast<uint2*>(sT + swz_t(dc * 8 + j, chunk) + hoff) =
+        make_uint2(__builtin_amdgcn_perm(w1[j >> 1], w0[j >> 1], sel), __builtin_amdgcn_perm(w3[j >> 1], w2[j >> 1], sel));
   }
 }
 
@@ -165,7 +165,8 @@ __global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
   constexpr int NBLK = (BQ / 4) * (DP / 8);         // 4 x 8 blocks per tile
   constexpr int BL = (NBLK + NTH - 1) / NTH;
   __shared__ __align__(16) uint8_t smem[4 * TILE];  // Q, Q^T, dO, dO^T
-  __shared__ float s_lse[BQ], s_delta[BQ];
+  __shared__ __align__(16) float s_lse[BQ];
+  __shared__ __align__(16) float s_delta[BQ];
   uint8_t* sQ = smem;
   uint8_t* sQT = smem + TILE;
   uint8_t* sD = smem + 2 * TILE;
@@ -259,30 +260,54 @@ __global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
         pacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, vf[s], pacc[qb], 0, 0, 0);
       }
     }
-    // P and dS (fp16, packed in MFMA k-slot order)
+    // P and dS (fp16, packed in MFMA k-slot order). The lane's 16 queries of a
+    // 32-query block are 4 runs of 4 (ql = 32 qb + 8 i + 4 fk + j): lse and delta
+    // come as float4s. Masking only where the tile crosses the diagonal or an end.
+    const bool edge = q0 + BQ > p.Sq || k0 + BK > p.Sk || (CAUSAL && k0 + wave * 32 + 31 >= q0);
+    // with a bias the logits are scaled and biased first, as in the forward pass
+    const float cs = HAS_BIAS ? 1.f : p.scale_log2;
+    if constexpr (HAS_BIAS) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = q0 + qb * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+          if (qi < p.Sq && key < p.Sk)
+            sacc[qb][r] = sacc[qb][r] * p.scale_log2 +
+                          (float)__builtin_bit_cast(_Float16, p.bias[(int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh +
+                                                                     (int64_t)qi * p.bias_sq + key]) * kLog2e;
+          else
+            sacc[qb][r] *= p.scale_log2;
+        }
+    }
+    if (edge) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = q0 + qb * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+          if (key >= p.Sk || qi >= p.Sq || (CAUSAL && key > qi)) sacc[qb][r] = -INFINITY;
+        }
+    }
     uint32_t pp[2][8], ds[2][8];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float pv[2], dsv[2];
+      for (int i = 0; i < 4; ++i) {
+        const int ql0 = qb * 32 + 8 * i + 4 * fk;
+        const float4 l4 = *reinterpret_cast<const float4*>(s_lse + ql0);
+        const float4 d4 = *reinterpret_cast<const float4*>(s_delta + ql0);
+        const float lse4[4] = {l4.x, l4.y, l4.z, l4.w}, del4[4] = {d4.x, d4.y, d4.z, d4.w};
+        float pv[4], dsv[4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int ql = qb * 32 + 8 * ((r + u) >> 2) + 4 * fk + ((r + u) & 3);
-          const int qi = q0 + ql;
-          float s = sacc[qb][r + u] * p.scale_log2;
-          if constexpr (HAS_BIAS) {
-            if (qi < p.Sq && key < p.Sk)
-              s += (float)__builtin_bit_cast(_Float16, p.bias[(int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh +
-                                                              (int64_t)qi * p.bias_sq + key]) * kLog2e;
-          }
-          float pr = __builtin_amdgcn_exp2f(s - s_lse[ql]);
-          if (key >= p.Sk || qi >= p.Sq || (CAUSAL && key > qi)) pr = 0.f;
-          pv[u] = pr;
-          dsv[u] = pr * (pacc[qb][r + u] - s_delta[ql]);
+        for (int j = 0; j < 4; ++j) {
+          pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[qb][4 * i + j], cs, -lse4[j]));
+          dsv[j] = pv[j] * (pacc[qb][4 * i + j] - del4[j]);
         }
-        pp[qb][r >> 1] = pack_f16(pv[0], pv[1]);
-        ds[qb][r >> 1] = pack_f16(dsv[0], dsv[1]);
+        pp[qb][2 * i] = pack_f16(pv[0], pv[1]);
+        pp[qb][2 * i + 1] = pack_f16(pv[2], pv[3]);
+        ds[qb][2 * i] = pack_f16(dsv[0], dsv[1]);
+        ds[qb][2 * i + 1] = pack_f16(dsv[2], dsv[3]);
       }
     // dV += P^T dO16, dK += dS^T Q16 over four 16-query steps
 #pragma unroll
@@ -433,6 +458,28 @@ __global__ __launch_bounds__(NTH) void dq_kernel(BwdParams p) {
         pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, df[s], pacc[kh], 0, 0, 0);
       }
     }
+    // masking only where the tile crosses the diagonal or an end
+    const bool edge = kb * BKV + BKV > p.Sk || q0 + BQ > p.Sq || (CAUSAL && kb * BKV + BKV - 1 > q0 + wave * 32);
+    const float cs = HAS_BIAS ? 1.f : p.scale_log2;  // with a bias: scaled and biased first
+    if constexpr (HAS_BIAS) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = kb * BKV + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+          sacc[kh][r] = sacc[kh][r] * p.scale_log2 +
+                        (kk < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[kk]) * kLog2e : 0.f);
+        }
+    }
+    if (edge) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = kb * BKV + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+          if (kk >= p.Sk || qrow >= p.Sq || (CAUSAL && kk > qrow)) sacc[kh][r] = -INFINITY;
+        }
+    }
     uint32_t ds[2][8];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh)
@@ -441,13 +488,7 @@ __global__ __launch_bounds__(NTH) void dq_kernel(BwdParams p) {
         float dsv[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const int kk = kb * BKV + kh * 32 + 8 * ((r + u) >> 2) + 4 * fk + ((r + u) & 3);
-          float s = sacc[kh][r + u] * p.scale_log2;
-          if constexpr (HAS_BIAS) {
-            if (kk < p.Sk) s += (float)__builtin_bit_cast(_Float16, brow[kk]) * kLog2e;
-          }
-          float pr = __builtin_amdgcn_exp2f(s - lse_q);
-          if (kk >= p.Sk || qrow >= p.Sq || (CAUSAL && kk > qrow)) pr = 0.f;
+          const float pr = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r + u], cs, -lse_q));
           dsv[u] = pr * (pacc[kh][r + u] - delta_q);
         }
         ds[kh][r >> 1] = pack_f16(dsv[0], dsv[1]);
