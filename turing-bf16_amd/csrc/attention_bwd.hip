@@ -364,14 +364,19 @@ __global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
 }
 
 // ---- dQ --------------------------------------------------------------------------
+// Two blocks per CU (two waves per SIMD, without a bias): a wave's dO rows live in
+// a private LDS region instead of registers, and each 64-key tile is processed as
+// two 32-key halves, which keeps a wave within 256 registers.
 template <int DP, bool CAUSAL, bool HAS_BIAS>
-__global__ __launch_bounds__(NTH) void dq_kernel(BwdParams p) {
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS ? 1 : 2, HAS_BIAS ? 1 : 2))) void
+dq_kernel(BwdParams p) {
   constexpr int BQ = 128, BKV = 64;
   constexpr int KS = DP / 16, DB = DP / 32;
   constexpr int TILE = BKV * DP * 2;
   constexpr int NBLK = (BKV / 4) * (DP / 8);
   constexpr int BL = (NBLK + NTH - 1) / NTH;
-  __shared__ __align__(16) uint8_t smem[3 * TILE];  // K, K^T, V (+ V^T slot unused)
+  constexpr int DOW = 32 * DP * 2;  // one wave's dO rows
+  __shared__ __align__(16) uint8_t smem[3 * TILE + 4 * DOW];  // K, K^T, V, dO (per wave)
   uint8_t* sK = smem;
   uint8_t* sKT = smem + TILE;
   uint8_t* sV = smem + 2 * TILE;
@@ -385,7 +390,8 @@ __global__ __launch_bounds__(NTH) void dq_kernel(BwdParams p) {
   const int G = p.exps_out[1];
 
   const int qrow = q0 + wave * 32 + fr;
-  half8 qf[KS], df[KS];
+  half8 qf[KS];
+  uint8_t* sDo = smem + 3 * TILE + wave * DOW;  // written and read by this wave only
   {
     const float sq = ldexp1(a), sdo = ldexp1(ev + G);
     const uint16_t* qr = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)min(qrow, p.Sq - 1) * p.q_ss;
@@ -395,7 +401,8 @@ __global__ __launch_bounds__(NTH) void dq_kernel(BwdParams p) {
       const int d = 16 * s + 8 * fk;
       const bool ok = qrow < p.Sq && d < p.D;
       qf[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(qr + d), sq) : make_uint4(0, 0, 0, 0));
-      df[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(dr + d), sdo) : make_uint4(0, 0, 0, 0));
+      *reinterpret_cast<uint4*>(sDo + swz_row<DP>(fr, 2 * s + fk)) =
+          ok ? cvt_bf16x8_f16x8(ldg16(dr + d), sdo) : make_uint4(0, 0, 0, 0);
     }
   }
   const float lse_q = qrow < p.Sq ? p.lse[(int64_t)bh * p.Sq + qrow] : INFINITY;
@@ -444,63 +451,54 @@ __global__ __launch_bounds__(NTH) void dq_kernel(BwdParams p) {
     __syncthreads();
     if (kb + 1 < nkb) gload(kb + 1);
 
-    // S^T and dP^T: lane = one query, 16 keys per 32-key half
-    floatx16 sacc[2], pacc[2];
+    // per 32-key half: S^T and dP^T (lane = one query, 16 keys), then dS and its
+    // two 16-key steps of dQ^T += K^T dS^T
+    const float cs = HAS_BIAS ? 1.f : p.scale_log2;  // with a bias: scaled and biased first
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
+      floatx16 sacc, pacc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kh][r] = pacc[kh][r] = 0.f;
+      for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const half8 ka = *reinterpret_cast<const half8*>(sK + swz_row<DP>(kh * 32 + fr, 2 * s + fk));
         const half8 va = *reinterpret_cast<const half8*>(sV + swz_row<DP>(kh * 32 + fr, 2 * s + fk));
-        sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[s], sacc[kh], 0, 0, 0);
-        pacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, df[s], pacc[kh], 0, 0, 0);
+        const half8 dfs = *reinterpret_cast<const half8*>(sDo + swz_row<DP>(fr, 2 * s + fk));
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[s], sacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, dfs, pacc, 0, 0, 0);
       }
-    }
-    // masking only where the tile crosses the diagonal or an end
-    const bool edge = kb * BKV + BKV > p.Sk || q0 + BQ > p.Sq || (CAUSAL && kb * BKV + BKV - 1 > q0 + wave * 32);
-    const float cs = HAS_BIAS ? 1.f : p.scale_log2;  // with a bias: scaled and biased first
-    if constexpr (HAS_BIAS) {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
+      const int kb0 = kb * BKV + kh * 32;
+      if constexpr (HAS_BIAS) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int kk = kb * BKV + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-          sacc[kh][r] = sacc[kh][r] * p.scale_log2 +
-                        (kk < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[kk]) * kLog2e : 0.f);
+          const int kk = kb0 + 8 * (r >> 2) + 4 * fk + (r & 3);
+          sacc[r] = sacc[r] * p.scale_log2 + (kk < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[kk]) * kLog2e : 0.f);
         }
-    }
-    if (edge) {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
+      }
+      // masking only where the half crosses the diagonal or an end
+      if (kb0 + 32 > p.Sk || q0 + BQ > p.Sq || (CAUSAL && kb0 + 31 > q0 + wave * 32)) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int kk = kb * BKV + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-          if (kk >= p.Sk || qrow >= p.Sq || (CAUSAL && kk > qrow)) sacc[kh][r] = -INFINITY;
+          const int kk = kb0 + 8 * (r >> 2) + 4 * fk + (r & 3);
+          if (kk >= p.Sk || qrow >= p.Sq || (CAUSAL && kk > qrow)) sacc[r] = -INFINITY;
         }
-    }
-    uint32_t ds[2][8];
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
+      }
+      uint32_t ds[8];
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        float dsv[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const float pr = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r + u], cs, -lse_q));
-          dsv[u] = pr * (pacc[kh][r + u] - delta_q);
-        }
-        ds[kh][r >> 1] = pack_f16(dsv[0], dsv[1]);
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[r], cs, -lse_q));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[r + 1], cs, -lse_q));
+        ds[r >> 1] = pack_f16(p0 * (pacc[r] - delta_q), p1 * (pacc[r + 1] - delta_q));
       }
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int kh = ks >> 1, o = 4 * (ks & 1);
-      const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[kh][o], ds[kh][o + 1], ds[kh][o + 2], ds[kh][o + 3]));
+      for (int kq = 0; kq < 2; ++kq) {
+        const int ks = 2 * kh + kq, o = 4 * kq;
+        const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[o], ds[o + 1], ds[o + 2], ds[o + 3]));
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const half8 kbf = *reinterpret_cast<const half8*>(sKT + swz_t(db * 32 + fr, 2 * ks + fk));
-        dq[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbf, sa, dq[db], 0, 0, 0);
+        for (int db = 0; db < DB; ++db) {
+          const half8 kbf = *reinterpret_cast<const half8*>(sKT + swz_t(db * 32 + fr, 2 * ks + fk));
+          dq[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbf, sa, dq[db], 0, 0, 0);
+        }
       }
     }
   }
