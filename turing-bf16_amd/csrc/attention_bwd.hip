@@ -156,21 +156,54 @@ __device__ __forceinline__ void store_blk_both(uint8_t* sRow, uint8_t* sT, const
   }
 }
 
+// Byte offset of the 8-byte run starting at column col (a multiple of 4) of row
+// row in a row-major, 16-byte-chunk-swizzled DP-wide fp16 tile.
+template <int DP>
+__device__ __forceinline__ int swz_run8(int row, int col) {
+  return swz_row<DP>(row, col >> 3) + ((col >> 2) & 1) * 8;
+}
+
+// MFMA B fragment (32 columns n x 16 k) of the TRANSPOSE of a row-major tile, read
+// with two ds_read_b64_tr_b16: for lane L (n = L % 32, k group g = L / 32), k slot
+// t holds tile[r0 + 4 g + (t & 3) + 8 (t >> 2)][c0 + n], the same k order as an
+// accumulator-derived A fragment (rows 8 (t / 4) + 4 g + t % 4 of a 16-row step).
+// Within each 16-lane group the instruction hands element j of lane 4 a + b the
+// b-th half of the 8 bytes addressed by lane a + 4 j, so each lane addresses row
+// r0 + 4 g + ((L / 4) % 4) + 8 h, columns c0 + 16 ((L / 16) % 2) + 4 (L % 4).
+template <int DP>
+__device__ __forceinline__ half8 tr_frag(const uint8_t* tile, int r0, int c0, int lane) {
+  const int row = r0 + 4 * (lane >> 5) + ((lane >> 2) & 3);
+  const int col = c0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(tile + swz_run8<DP>(row, col)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(tile + swz_run8<DP>(row + 8, col)));
+  return __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // ---- dK, dV --------------------------------------------------------------------
+// Block = 128 keys (32 per wave, K16 fragments in registers, the wave's V16 rows
+// in a private LDS region), loop over 64-query tiles (and over the query heads of
+// a GQA group). Q16 and dO16 tiles sit in LDS once, row-major: they are the A
+// operand of S = Q K^T and dP = dO V^T (lane = ONE key, 16 queries), and their
+// transposes for dV += P^T dO and dK += dS^T Q come from ds_read_b64_tr_b16, so P
+// and dS feed the MFMAs straight from registers. Each tile is handled as two
+// 32-query halves; without a bias a wave stays within 256 registers and two
+// blocks share a CU.
 template <int DP, bool CAUSAL, bool HAS_BIAS>
-__global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS ? 1 : 2, HAS_BIAS ? 1 : 2))) void
+dkdv_kernel(BwdParams p) {
   constexpr int BQ = 64, BK = 128;
-  constexpr int KS = DP / 16, DB = DP / 32;
-  constexpr int TILE = BQ * DP * 2;                 // one 64 x DP fp16 tile
-  constexpr int NBLK = (BQ / 4) * (DP / 8);         // 4 x 8 blocks per tile
-  constexpr int BL = (NBLK + NTH - 1) / NTH;
-  __shared__ __align__(16) uint8_t smem[4 * TILE];  // Q, Q^T, dO, dO^T
+  constexpr int KS = DP / 16, DB = DP / 32, CPR = DP / 8;
+  constexpr int TILE = BQ * DP * 2;   // one 64 x DP fp16 tile
+  constexpr int VW = 32 * DP * 2;     // one wave's V rows
+  constexpr int CH = BQ * CPR / NTH;  // 16-byte chunks per thread per tile
+  constexpr int MAIN = 4 * VW + 2 * TILE, OUT = BK * DP * 4;
+  __shared__ __align__(16) uint8_t smem[MAIN > OUT ? MAIN : OUT];
   __shared__ __align__(16) float s_lse[BQ];
   __shared__ __align__(16) float s_delta[BQ];
-  uint8_t* sQ = smem;
-  uint8_t* sQT = smem + TILE;
-  uint8_t* sD = smem + 2 * TILE;
-  uint8_t* sDT = smem + 3 * TILE;
+  uint8_t* sQ = smem + 4 * VW;
+  uint8_t* sD = sQ + TILE;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, fr = lane & 31, fk = lane >> 5;
   const int bk = blockIdx.y, b = bk / p.Hkv, hk = bk % p.Hkv;
@@ -179,9 +212,11 @@ __global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
   const int ev = p.exps_fwd[2 + bk];
   const int G = p.exps_out[1];
 
-  // wave's 32 keys as fragments (B operand of S = Q K^T and dP = dO V^T)
+  // wave's 32 keys: K16 fragments (B operand of S = Q K^T) in registers, V16 rows
+  // (B operand of dP = dO V^T) in this wave's LDS region
   const int key = k0 + wave * 32 + fr;
-  half8 kf[KS], vf[KS];
+  half8 kf[KS];
+  uint8_t* sVw = smem + wave * VW;
   {
     const float sk = ldexp1(-a), sv = ldexp1(-ev);
     const uint16_t* kr = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)min(key, p.Sk - 1) * p.k_ss;
@@ -191,7 +226,8 @@ __global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
       const int d = 16 * s + 8 * fk;
       const bool ok = key < p.Sk && d < p.D;
       kf[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(kr + d), sk) : make_uint4(0, 0, 0, 0));
-      vf[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(vr + d), sv) : make_uint4(0, 0, 0, 0));
+      *reinterpret_cast<uint4*>(sVw + swz_row<DP>(fr, 2 * s + fk)) =
+          ok ? cvt_bf16x8_f16x8(ldg16(vr + d), sv) : make_uint4(0, 0, 0, 0);
     }
   }
   floatx16 dk[DB], dv[DB];
@@ -205,38 +241,37 @@ __global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
   const int qt0 = CAUSAL ? min(k0 / BQ, nqt) : 0;
   const int total = group * (nqt - qt0);
 
-  uint4 rq[BL][4], rd[BL][4];
+  // tile staging: thread t moves 16-byte chunks t + 256 i (row c / CPR, chunk c % CPR)
+  // of the Q and dO tiles; rows past Sq and columns past D load as zeros
+  uint4 rq[CH], rd[CH];
   auto gload = [&](int it) {
     const int h = hk * group + it / (nqt - qt0);
     const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
     const uint16_t* qb = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
     const uint16_t* db = p.dout + (int64_t)b * p.d_sb + (int64_t)h * p.d_sh;
 #pragma unroll
-    for (int i = 0; i < BL; ++i) {
-      const int blk = tid + i * NTH;
-      const int kg = blk & 15, dc = blk >> 4;
-      if (blk < NBLK) {
-        load_blk(qb, p.q_ss, q0 + 4 * kg, p.Sq, dc * 8, p.D, rq[i]);
-        load_blk(db, p.d_ss, q0 + 4 * kg, p.Sq, dc * 8, p.D, rd[i]);
-      }
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
+      const bool ok = q0 + row < p.Sq && ch * 8 < p.D;
+      rq[i] = ok ? ldg16(qb + (int64_t)(q0 + row) * p.q_ss + ch * 8) : make_uint4(0, 0, 0, 0);
+      rd[i] = ok ? ldg16(db + (int64_t)(q0 + row) * p.d_ss + ch * 8) : make_uint4(0, 0, 0, 0);
     }
   };
 
-  if (total > 0) gload(0);
   for (int it = 0; it < total; ++it) {
     const int h = hk * group + it / (nqt - qt0);
     const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
     const int bh = b * p.H + h;
     const float sq = ldexp1(a), sdo = ldexp1(ev + G);
-    __syncthreads();  // previous tile's readers are done
+    // no register prefetch (it would cost the second block per CU): the loads are
+    // issued before the barrier that waits for the previous tile's readers
+    gload(it);
+    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < BL; ++i) {
-      const int blk = tid + i * NTH;
-      const int kg = blk & 15, dc = blk >> 4;
-      if (blk < NBLK) {
-        store_blk_both<DP>(sQ, sQT, rq[i], sq, 4 * kg, dc);
-        store_blk_both<DP>(sD, sDT, rd[i], sdo, 4 * kg, dc);
-      }
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
+      *reinterpret_cast<uint4*>(sQ + swz_row<DP>(row, ch)) = cvt_bf16x8_f16x8(rq[i], sq);
+      *reinterpret_cast<uint4*>(sD + swz_row<DP>(row, ch)) = cvt_bf16x8_f16x8(rd[i], sdo);
     }
     if (tid < BQ) {
       const int qi = q0 + tid;
@@ -244,54 +279,47 @@ __global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
       s_delta[tid] = qi < p.Sq ? p.delta[(int64_t)bh * p.Sq + qi] : 0.f;
     }
     __syncthreads();
-    if (it + 1 < total) gload(it + 1);
 
-    // S and dP for two 32-query blocks: lane = one key, 16 queries each
-    floatx16 sacc[2], pacc[2];
+    const bool edge = q0 + BQ > p.Sq || k0 + BK > p.Sk || (CAUSAL && k0 + wave * 32 + 31 >= q0);
+    // with a bias the logits are scaled and biased first, as in the forward pass
+    const float cs = HAS_BIAS ? 1.f : p.scale_log2;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
+      // S and dP for 32 queries: lane = one key, 16 queries
+      floatx16 sacc, pacc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[qb][r] = pacc[qb][r] = 0.f;
+      for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const half8 qa = *reinterpret_cast<const half8*>(sQ + swz_row<DP>(qb * 32 + fr, 2 * s + fk));
         const half8 da = *reinterpret_cast<const half8*>(sD + swz_row<DP>(qb * 32 + fr, 2 * s + fk));
-        sacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kf[s], sacc[qb], 0, 0, 0);
-        pacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, vf[s], pacc[qb], 0, 0, 0);
+        const half8 vb = *reinterpret_cast<const half8*>(sVw + swz_row<DP>(fr, 2 * s + fk));
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kf[s], sacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, vb, pacc, 0, 0, 0);
       }
-    }
-    // P and dS (fp16, packed in MFMA k-slot order). The lane's 16 queries of a
-    // 32-query block are 4 runs of 4 (ql = 32 qb + 8 i + 4 fk + j): lse and delta
-    // come as float4s. Masking only where the tile crosses the diagonal or an end.
-    const bool edge = q0 + BQ > p.Sq || k0 + BK > p.Sk || (CAUSAL && k0 + wave * 32 + 31 >= q0);
-    // with a bias the logits are scaled and biased first, as in the forward pass
-    const float cs = HAS_BIAS ? 1.f : p.scale_log2;
-    if constexpr (HAS_BIAS) {
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+      if constexpr (HAS_BIAS) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int qi = q0 + qb * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
           if (qi < p.Sq && key < p.Sk)
-            sacc[qb][r] = sacc[qb][r] * p.scale_log2 +
-                          (float)__builtin_bit_cast(_Float16, p.bias[(int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh +
-                                                                     (int64_t)qi * p.bias_sq + key]) * kLog2e;
+            sacc[r] = sacc[r] * p.scale_log2 +
+                      (float)__builtin_bit_cast(_Float16, p.bias[(int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh +
+                                                                 (int64_t)qi * p.bias_sq + key]) * kLog2e;
           else
-            sacc[qb][r] *= p.scale_log2;
+            sacc[r] *= p.scale_log2;
         }
-    }
-    if (edge) {
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+      }
+      // masking only where the tile crosses the diagonal or an end
+      if (edge) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int qi = q0 + qb * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-          if (key >= p.Sk || qi >= p.Sq || (CAUSAL && key > qi)) sacc[qb][r] = -INFINITY;
+          if (key >= p.Sk || qi >= p.Sq || (CAUSAL && key > qi)) sacc[r] = -INFINITY;
         }
-    }
-    uint32_t pp[2][8], ds[2][8];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+      }
+      // P and dS (fp16, packed in MFMA k-slot order); the lane's 16 queries are 4
+      // runs of 4 (q = 32 qb + 8 i + 4 fk + j), so lse and delta come as float4s
+      uint32_t pp[8], ds[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int ql0 = qb * 32 + 8 * i + 4 * fk;
@@ -301,26 +329,27 @@ __global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
         float pv[4], dsv[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[qb][4 * i + j], cs, -lse4[j]));
-          dsv[j] = pv[j] * (pacc[qb][4 * i + j] - del4[j]);
+          pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[4 * i + j], cs, -lse4[j]));
+          dsv[j] = pv[j] * (pacc[4 * i + j] - del4[j]);
         }
-        pp[qb][2 * i] = pack_f16(pv[0], pv[1]);
-        pp[qb][2 * i + 1] = pack_f16(pv[2], pv[3]);
-        ds[qb][2 * i] = pack_f16(dsv[0], dsv[1]);
-        ds[qb][2 * i + 1] = pack_f16(dsv[2], dsv[3]);
+        pp[2 * i] = pack_f16(pv[0], pv[1]);
+        pp[2 * i + 1] = pack_f16(pv[2], pv[3]);
+        ds[2 * i] = pack_f16(dsv[0], dsv[1]);
+        ds[2 * i + 1] = pack_f16(dsv[2], dsv[3]);
       }
-    // dV += P^T dO16, dK += dS^T Q16 over four 16-query steps
+      // dV += P^T dO16, dK += dS^T Q16 over the half's two 16-query steps
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int qb = ks >> 1, o = 4 * (ks & 1);
-      const half8 pa = __builtin_bit_cast(half8, make_uint4(pp[qb][o], pp[qb][o + 1], pp[qb][o + 2], pp[qb][o + 3]));
-      const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[qb][o], ds[qb][o + 1], ds[qb][o + 2], ds[qb][o + 3]));
+      for (int kq = 0; kq < 2; ++kq) {
+        const int o = 4 * kq, r0 = qb * 32 + 16 * kq;
+        const half8 pa = __builtin_bit_cast(half8, make_uint4(pp[o], pp[o + 1], pp[o + 2], pp[o + 3]));
+        const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[o], ds[o + 1], ds[o + 2], ds[o + 3]));
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const half8 dob = *reinterpret_cast<const half8*>(sDT + swz_t(db * 32 + fr, 2 * ks + fk));
-        const half8 qbf = *reinterpret_cast<const half8*>(sQT + swz_t(db * 32 + fr, 2 * ks + fk));
-        dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, dob, dv[db], 0, 0, 0);
-        dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, qbf, dk[db], 0, 0, 0);
+        for (int db = 0; db < DB; ++db) {
+          const half8 dob = tr_frag<DP>(sD, r0, db * 32, lane);
+          const half8 qbf = tr_frag<DP>(sQ, r0, db * 32, lane);
+          dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, dob, dv[db], 0, 0, 0);
+          dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, qbf, dk[db], 0, 0, 0);
+        }
       }
     }
   }
@@ -329,7 +358,7 @@ __global__ __launch_bounds__(NTH) void dkdv_kernel(BwdParams p) {
   // dV / dK accumulators are C[key][d] with key = MFMA row: lane holds col d = fr and
   // rows key = 8*(r/4) + 4*fk + r%4. Transpose through LDS for 16-byte stores.
   __syncthreads();
-  float* sOut = reinterpret_cast<float*>(smem);  // 128 keys x DP floats per pass (<= 4 * TILE bytes)
+  float* sOut = reinterpret_cast<float*>(smem);  // 128 keys x DP floats per pass
   const float sk_out = ldexp1(-a - G) * p.scale, sv_out = ldexp1(-ev - G);
   bool bad = false;
   for (int pass = 0; pass < 2; ++pass) {
