@@ -14,16 +14,17 @@
 //
 // Kernels (4 waves, v_mfma_f32_32x32x16_f16):
 //   delta:   one 16-lane group per query row; also computes e, G.
-//   dkdv:    block = 128 keys (32 per wave, K16 / V16 fragments in registers), loops
-//            over 64-query tiles (and over the query heads of a GQA group). Q and
-//            dO tiles sit in LDS twice: row-major (A operand of S = Q K^T and
-//            dP = dO V^T, whose accumulators give each lane ONE key and 16 queries)
-//            and transposed with queries permuted in 16-groups (B operand of
-//            dV += P^T dO and dK += dS^T Q), so P / dS feed the next MFMA
-//            straight from registers.
-//   dq:      block = 128 queries (32 per wave, Q16 / dO16 in registers), loops over
-//            64-key tiles: K row-major + transposed and V row-major in LDS; S^T and
-//            dP^T give each lane ONE query, so dS is the A operand of dQ += dS K.
+//   dkdv:    block = 128 keys (32 per wave, K16 fragments in registers, V16 rows in
+//            per-wave LDS), loops over 64-query tiles (and over the query heads
+//            of a GQA group). Q and dO tiles sit in LDS row-major: the A operand
+//            of S = Q K^T and dP = dO V^T (accumulators: each lane ONE key, 16
+//            queries), and via ds_read_b64_tr_b16 the transposed B operand of
+//            dV += P^T dO and dK += dS^T Q, so P / dS feed the MFMAs straight
+//            from registers.
+//   dq:      block = 128 queries (32 per wave, Q16 in registers, dO16 in per-wave
+//            LDS), loops over 64-key tiles: K and V row-major in LDS; S^T and dP^T
+//            give each lane ONE query, and dQ^T += K^T dS^T takes K^T fragments
+//            from ds_read_b64_tr_b16.
 #include <algorithm>
 #include <math.h>
 
@@ -63,14 +64,6 @@ struct BwdParams {
   uint16_t *dq, *dk, *dv;
 };
 
-__device__ __forceinline__ int perm16(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
-
-template <int DP>
-__device__ __forceinline__ int swz_row(int row, int chunk) {
-  if constexpr (DP >= 128) return row * (DP * 2) + ((chunk ^ (row & 15)) << 4);
-  else return row * (DP * 2) + ((chunk ^ ((row >> 1) & 7)) << 4);
-}
-__device__ __forceinline__ int swz_t(int d, int chunk) { return d * 128 + ((chunk ^ ((d >> 1) & 7)) << 4); }
 
 __device__ __forceinline__ int ev_of(const BwdParams& p, int b, int h) {
   return p.exps_fwd[2 + b * p.Hkv + h / (p.H / p.Hkv)];
@@ -121,64 +114,6 @@ __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
 #pragma unroll
   for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
   if (row < p.Sq && l16 == 0) p.delta[(int64_t)bh * p.Sq + row] = acc;
-}
-
-// Loads a 4-row x 8-column bf16 block (rows r0..r0+3 of a strided matrix) as raw uint4s.
-__device__ __forceinline__ void load_blk(const uint16_t* base, int64_t rs, int r0, int rows, int d, int D, uint4 (&v)[4]) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-    v[r] = (r0 + r < rows && d < D) ? ldg16(base + (int64_t)(r0 + r) * rs + d) : make_uint4(0, 0, 0, 0);
-}
-
-// Converts a block with scale s and writes it row-major (rows r0l..r0l+3, chunk dc) and
-// transposed (d-major rows dc*8..dc*8+7, columns perm16(r0l..r0l+3)) into LDS.
-template <int DP>
-__device__ __forceinline__ void store_blk_both(uint8_t* sRow, uint8_t* sT, const uint4 (&raw)[4], float s, int r0l,
-                                               int dc) {
-  uint4 cv[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    cv[r] = cvt_bf16x8_f16x8(raw[r], s);
-    *reinterpret_cast<uint4*>(sRow + swz_row<DP>(r0l + r, dc)) = cv[r];
-  }
-  const int pos = perm16(r0l);
-  const int chunk = pos >> 3, hoff = (pos & 7) * 2;
-  const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
-  const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
-  const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&cv[2]);
-  const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    // halves j of the four rows -> one 4-element run, two v_perm_b32
-    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-    *reinterpret_cast<uint2*>(sT + swz_t(dc * 8 + j, chunk) + hoff) =
-        make_uint2(__builtin_amdgcn_perm(w1[j >> 1], w0[j >> 1], sel), __builtin_amdgcn_perm(w3[j >> 1], w2[j >> 1], sel));
-  }
-}
-
-// Byte offset of the 8-byte run starting at column col (a multiple of 4) of row
-// row in a row-major, 16-byte-chunk-swizzled DP-wide fp16 tile.
-template <int DP>
-__device__ __forceinline__ int swz_run8(int row, int col) {
-  return swz_row<DP>(row, col >> 3) + ((col >> 2) & 1) * 8;
-}
-
-// MFMA B fragment (32 columns n x 16 k) of the TRANSPOSE of a row-major tile, read
-// with two ds_read_b64_tr_b16: for lane L (n = L % 32, k group g = L / 32), k slot
-// t holds tile[r0 + 4 g + (t & 3) + 8 (t >> 2)][c0 + n], the same k order as an
-// accumulator-derived A fragment (rows 8 (t / 4) + 4 g + t % 4 of a 16-row step).
-// Within each 16-lane group the instruction hands element j of lane 4 a + b the
-// b-th half of the 8 bytes addressed by lane a + 4 j, so each lane addresses row
-// r0 + 4 g + ((L / 4) % 4) + 8 h, columns c0 + 16 ((L / 16) % 2) + 4 (L % 4).
-template <int DP>
-__device__ __forceinline__ half8 tr_frag(const uint8_t* tile, int r0, int c0, int lane) {
-  const int row = r0 + 4 * (lane >> 5) + ((lane >> 2) & 3);
-  const int col = c0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  typedef short v4s __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) v4s lds_v4s;
-  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(tile + swz_run8<DP>(row, col)));
-  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(tile + swz_run8<DP>(row + 8, col)));
-  return __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // ---- dK, dV --------------------------------------------------------------------
@@ -402,13 +337,11 @@ dq_kernel(BwdParams p) {
   constexpr int BQ = 128, BKV = 64;
   constexpr int KS = DP / 16, DB = DP / 32;
   constexpr int TILE = BKV * DP * 2;
-  constexpr int NBLK = (BKV / 4) * (DP / 8);
-  constexpr int BL = (NBLK + NTH - 1) / NTH;
+  constexpr int CPR = DP / 8, CH = BKV * CPR / NTH;  // 16-byte chunks per thread per tile
   constexpr int DOW = 32 * DP * 2;  // one wave's dO rows
-  __shared__ __align__(16) uint8_t smem[3 * TILE + 4 * DOW];  // K, K^T, V, dO (per wave)
+  __shared__ __align__(16) uint8_t smem[2 * TILE + 4 * DOW];  // K, V, dO (per wave)
   uint8_t* sK = smem;
-  uint8_t* sKT = smem + TILE;
-  uint8_t* sV = smem + 2 * TILE;
+  uint8_t* sV = smem + TILE;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, fr = lane & 31, fk = lane >> 5;
   const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H, hk = h / (p.H / p.Hkv);
@@ -420,7 +353,7 @@ dq_kernel(BwdParams p) {
 
   const int qrow = q0 + wave * 32 + fr;
   half8 qf[KS];
-  uint8_t* sDo = smem + 3 * TILE + wave * DOW;  // written and read by this wave only
+  uint8_t* sDo = smem + 2 * TILE + wave * DOW;  // written and read by this wave only
   {
     const float sq = ldexp1(a), sdo = ldexp1(ev + G);
     const uint16_t* qr = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)min(qrow, p.Sq - 1) * p.q_ss;
@@ -447,16 +380,16 @@ dq_kernel(BwdParams p) {
   const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
   const uint16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
   const float sk = ldexp1(-a), sv = ldexp1(-ev);
-  uint4 rk[BL][4], rv[BL][4];
+  // tile staging: thread t moves 16-byte chunks t + 256 i (row c / CPR, chunk
+  // c % CPR) of the K and V tiles; rows past Sk and columns past D load as zeros
+  uint4 rk[CH], rv[CH];
   auto gload = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < BL; ++i) {
-      const int blk = tid + i * NTH;
-      const int kg = blk & 15, dc = blk >> 4;
-      if (blk < NBLK) {
-        load_blk(kbase, p.k_ss, kb * BKV + 4 * kg, p.Sk, dc * 8, p.D, rk[i]);
-        load_blk(vbase, p.v_ss, kb * BKV + 4 * kg, p.Sk, dc * 8, p.D, rv[i]);
-      }
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + i * NTH, row = kb * BKV + c / CPR, ch = c % CPR;
+      const bool ok = row < p.Sk && ch * 8 < p.D;
+      rk[i] = ok ? ldg16(kbase + (int64_t)row * p.k_ss + ch * 8) : make_uint4(0, 0, 0, 0);
+      rv[i] = ok ? ldg16(vbase + (int64_t)row * p.v_ss + ch * 8) : make_uint4(0, 0, 0, 0);
     }
   };
   const uint16_t* brow = nullptr;
@@ -467,15 +400,10 @@ dq_kernel(BwdParams p) {
   for (int kb = 0; kb < nkb; ++kb) {
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < BL; ++i) {
-      const int blk = tid + i * NTH;
-      const int kg = blk & 15, dc = blk >> 4;
-      if (blk < NBLK) {
-        store_blk_both<DP>(sK, sKT, rk[i], sk, 4 * kg, dc);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          *reinterpret_cast<uint4*>(sV + swz_row<DP>(4 * kg + r, dc)) = cvt_bf16x8_f16x8(rv[i][r], sv);
-      }
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
+      *reinterpret_cast<uint4*>(sK + swz_row<DP>(row, ch)) = cvt_bf16x8_f16x8(rk[i], sk);
+      *reinterpret_cast<uint4*>(sV + swz_row<DP>(row, ch)) = cvt_bf16x8_f16x8(rv[i], sv);
     }
     __syncthreads();
     if (kb + 1 < nkb) gload(kb + 1);
@@ -525,7 +453,7 @@ dq_kernel(BwdParams p) {
         const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[o], ds[o + 1], ds[o + 2], ds[o + 3]));
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const half8 kbf = *reinterpret_cast<const half8*>(sKT + swz_t(db * 32 + fr, 2 * ks + fk));
+          const half8 kbf = tr_frag<DP>(sK, 16 * ks, db * 32, lane);  // K^T fragment
           dq[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbf, sa, dq[db], 0, 0, 0);
         }
       }

@@ -123,6 +123,45 @@ __device__ __forceinline__ uint4 buf_load16(BufRes r, int voffset, int soffset) 
   return __builtin_bit_cast(uint4, raw_buffer_load_b128(d, voffset, __builtin_amdgcn_readfirstlane(soffset), 0));
 }
 
+// ---- LDS tiles ---------------------------------------------------------------
+
+// Byte offset of 16-byte chunk `chunk` of row `row` in a row-major DP-wide fp16 LDS
+// tile, the chunk index XOR-swizzled by row so that 16 lanes reading one chunk of
+// 16 consecutive rows (ds_read_b128 fragments) hit distinct banks: by row % 16
+// for 256-byte (or longer) rows, by (row / 2) % 8 for 128-byte rows.
+template <int DP>
+__device__ __forceinline__ int swz_row(int row, int chunk) {
+  if constexpr (DP >= 128) return row * (DP * 2) + ((chunk ^ (row & 15)) << 4);
+  else return row * (DP * 2) + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+
+// Byte offset of the 8-byte run starting at column col (a multiple of 4).
+template <int DP>
+__device__ __forceinline__ int swz_run8(int row, int col) {
+  return swz_row<DP>(row, col >> 3) + ((col >> 2) & 1) * 8;
+}
+
+// MFMA operand fragment (32 columns n x 16 k, either operand of
+// v_mfma_f32_32x32x16_f16) of the TRANSPOSE of a row-major swizzled tile, read
+// with two ds_read_b64_tr_b16 (gfx950): for lane L (n = L % 32, k group g = L / 32)
+// k slot t holds tile[r0 + 4 g + (t & 3) + 8 (t >> 2)][c0 + n]. That k order is the
+// one of a fragment packed from accumulators (rows 8 (t / 4) + 4 g + t % 4 of a
+// 16-row step), so P or dS can be the other operand straight from registers.
+// Within each 16-lane group the instruction gives element j of lane 4 a + b the
+// b-th half of the 8 bytes addressed by lane a + 4 j; hence lane L addresses row
+// r0 + 4 g + ((L / 4) % 4) (+ 8 for the second read), columns
+// c0 + 16 ((L / 16) % 2) + 4 (L % 4).
+template <int DP>
+__device__ __forceinline__ half8 tr_frag(const uint8_t* tile, int r0, int c0, int lane) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  const int row = r0 + 4 * (lane >> 5) + ((lane >> 2) & 3);
+  const int col = c0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(tile + swz_run8<DP>(row, col)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(tile + swz_run8<DP>(row + 8, col)));
+  return __builtin_bit_cast(half8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void stg16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 
