@@ -106,7 +106,7 @@ def bench_attention(S: int, iters: int):
     q, k, v = (t.to(dev) for t in W.cfg4_attention(S))
     B, H, _, D = q.shape
     flops = 2.0 * B * H * S * S * D  # causal: half of 4 B H S^2 D
-    for _ in range(2):
+    for _ in range(max(2, iters // 2)):
         tbf16.sdpa(q, k, v, is_causal=True)
     ms = _events_time(lambda: tbf16.sdpa(q, k, v, is_causal=True), iters)
     return {"S": S, "ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "pct_peak": 100 * flops / (ms * 1e-3) / 1e12 /
@@ -137,9 +137,22 @@ def bench_small_m(iters: int):
             step()
         ms = _events_time(step, iters * copies)
         byt = 2 * N * K + 2 * M * K + 2 * M * N + 4 * N + 4 * M
+        # the same calls replayed from a HIP graph (one per weight copy): device time
+        # without the Python call overhead, as a serving loop that captures decode sees it
+        ys = [tbf16.scaled_linear(xd, ws16[c], ws) for c in range(copies)]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            gy = [tbf16.scaled_linear(xd, ws16[c], ws) for c in range(copies)]
+        g.replay()
+        torch.cuda.synchronize()
+        if not all(torch.equal(a, b) for a, b in zip(ys, gy)):
+            raise RuntimeError(f"graph replay differs from the eager result at M={M}")
+        gms = _events_time(g.replay, iters) / copies
         out[str(M)] = {"us": round(ms * 1e3, 2), "GBs": round(byt / (ms * 1e-3) / 1e9, 1),
                        "pct_hbm": round(100 * byt / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
-                       "tflops": round(2 * M * N * K / (ms * 1e-3) / 1e12, 2)}
+                       "tflops": round(2 * M * N * K / (ms * 1e-3) / 1e12, 2),
+                       "graph_us": round(gms * 1e3, 2), "graph_GBs": round(byt / (gms * 1e-3) / 1e9, 1),
+                       "graph_pct_hbm": round(100 * byt / (gms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1)}
     return out
 
 
@@ -253,6 +266,8 @@ def profile_run(what: str):
             q, k, v = (t.to(dev) for t in W.cfg4_attention(S))
             for _ in range(3):
                 tbf16.sdpa(q, k, v, is_causal=True)
+    elif what == "train":
+        bench_train(2)
     else:
         bench_small_m(2)
     torch.cuda.synchronize()
@@ -275,10 +290,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=200)  # ~30 ms: lets the clocks settle
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline GEMM only")
-    ap.add_argument("--profile", choices=["gemm", "attention", "small_m"], default=None,
+    ap.add_argument("--profile", choices=["gemm", "attention", "small_m", "train"], default=None,
                     help="run a few launches of one workload for rocprofv3 and exit (no JSON); 'gemm' also runs a "
                          "256 MiB device copy that calibrates FETCH_SIZE / WRITE_SIZE")
     a = ap.parse_args()
@@ -299,7 +314,7 @@ def main():
           flush=True)
     extras = {}
     if not a.quick:
-        extras["attention_fwd"] = [bench_attention(S, it) for S, it in ((4096, 20), (16384, 5))]
+        extras["attention_fwd"] = [bench_attention(S, it) for S, it in ((4096, 60), (16384, 20))]
         print(f"[bench] attention {extras['attention_fwd']}", file=sys.stderr, flush=True)
         extras["small_m_decode"] = bench_small_m(20)
         print(f"[bench] small-M {extras['small_m_decode']}", file=sys.stderr, flush=True)
