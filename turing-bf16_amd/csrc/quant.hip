@@ -138,6 +138,7 @@ __global__ __launch_bounds__(256) void col_amax_partial_kernel(const uint16_t* _
   const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
   const int64_t r1 = min(R, r0 + rows_per_chunk);
   float m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll 4
   for (int64_t r = r0; r < r1; ++r) {
     const uint4 v = ldg16(x + r * ldx + c8 * 8);
     const float f = rm ? fabsf(rm[r]) : 1.f;
@@ -156,15 +157,26 @@ __global__ __launch_bounds__(256) void col_amax_partial_kernel(const uint16_t* _
 }
 
 // Reduce the partials of each column, then p[c] and s_inv[c] (small_kernels.cu:172,181).
+// Block = 64 columns x 4 chunk groups (thread g = tid / 64 takes chunks g, g + 4,
+// ... with several loads in flight); the 4 group maxima meet in LDS.
 __global__ __launch_bounds__(256) void col_exps_kernel(const float* __restrict__ partial, int64_t nchunks, int64_t K,
                                                        int t, int32_t* __restrict__ cexp, float* __restrict__ s_inv) {
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (c >= K) return;
+  __shared__ float red[4][64];
+  const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + cl;
   float m = 0.f;
-  for (int64_t i = 0; i < nchunks; ++i) m = fmaxf(m, partial[i * K + c]);
-  const int p = pow2_exp(m, t);
-  cexp[c] = p;
-  s_inv[c] = ldexp1(-p);
+  if (c < K) {
+#pragma unroll 8
+    for (int64_t i = g; i < nchunks; i += 4) m = fmaxf(m, partial[i * K + c]);
+  }
+  red[g][cl] = m;
+  __syncthreads();
+  if (g == 0 && c < K) {
+    m = fmaxf(fmaxf(red[0][cl], red[1][cl]), fmaxf(red[2][cl], red[3][cl]));
+    const int p = pow2_exp(m, t);
+    cexp[c] = p;
+    s_inv[c] = ldexp1(-p);
+  }
 }
 
 __global__ void fill_kernel(float* __restrict__ p, int64_t n, float v) {
@@ -389,7 +401,7 @@ extern "C" int tbf16_quantize_cols_t(const void* x, int64_t R, int64_t K, int64_
     dim3 g1((unsigned)cdiv(cdiv(K, 8), 256), (unsigned)ch);
     col_amax_partial_kernel<<<g1, 256, 0, st>>>((const uint16_t*)x, row_mul, R, K, ldx, cdiv(R, ch), partial);
     TB_LAUNCH_CHECK("quantize_cols/amax");
-    col_exps_kernel<<<(unsigned)cdiv(K, 256), 256, 0, st>>>(partial, ch, K, t, cexp, s_inv);
+    col_exps_kernel<<<(unsigned)cdiv(K, 64), 256, 0, st>>>(partial, ch, K, t, cexp, s_inv);
     TB_LAUNCH_CHECK("quantize_cols/exps");
   } else {  // no rows: s_inv = 1 as the reference returns (small_kernels.cu:325)
     fill_kernel<<<(unsigned)cdiv(K, 256), 256, 0, st>>>(s_inv, K, 1.0f);
