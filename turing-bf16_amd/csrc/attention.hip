@@ -19,8 +19,9 @@
 //  - row sums l come from the fp16 P that enters the PV product (v_dot2 with
 //    ones), so the normalisation matches the weights actually applied.
 //  - output bf16(O / l * 2^ev) written from registers: one rounding.
-// Causal blocks are launched heaviest first; key tiles past the diagonal are
-// skipped, and only tiles crossing the diagonal or the end of the keys take the
+// Causal blocks are launched heaviest first, or (few blocks per CU) each takes a
+// heavy and a light query tile; key tiles past the diagonal are skipped, and
+// only tiles crossing the diagonal or the end of the keys take the
 // (wave-uniform) masking branch.
 #include <stdlib.h>
 
@@ -57,6 +58,7 @@ struct FwdParams {
   float* lse;
   uint16_t* o16;
   int32_t* exps;
+  int pair;  // causal: block x handles query tiles ntiles-1-x and x (balanced work per block)
 };
 
 __device__ __forceinline__ int perm16(int key) {  // swap bits 2 and 3 of a key index
@@ -154,8 +156,6 @@ attn_fwd_kernel(FwdParams p) {
   const int fr = lane & 31, fk = lane >> 5;
   const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
   const int hk = h / (p.H / p.Hkv);
-  const int qt = CAUSAL ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;
-  const int q0 = qt * BQW;
 
   // ---- exponents ----
   const int eq = heads_max_exp<NT>(p.part_q, p.B * p.H, p.nch_q, red);
@@ -172,233 +172,243 @@ attn_fwd_kernel(FwdParams p) {
   }
   const float sq = ldexp1(a), sk = ldexp1(-a), sv = ldexp1(-ev);
 
-  // ---- Q fragments in registers (fp16, scaled by 2^a) ----
-  const int qrow = q0 + wave * 32 + fr;
-  half8 qf[KS];
-  {
-    const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)min(qrow, p.Sq - 1) * p.q_ss;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int d = 16 * s + 8 * fk;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (qrow < p.Sq && d < p.D) v = cvt_bf16x8_f16x8(ldg16(qp + d), sq);
-      qf[s] = __builtin_bit_cast(half8, v);
-    }
-  }
-
-  // ---- K / V staging through buffer loads (rows past Sk load as zeros) ----
-  const BufRes kres = make_res(p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh,
-                               min<int64_t>((int64_t)p.Sk * p.k_ss * 2, 0x7fffffff));
-  const BufRes vres = make_res(p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh,
-                               min<int64_t>((int64_t)p.Sk * p.v_ss * 2, 0x7fffffff));
-  const bool k_stager = NW != 8 || tid < KTH;
-  const bool v_stager = NW != 8 || tid >= VT0;
-  const int ktid = NW == 8 ? tid : tid, vtid = tid - VT0;
-  uint4 st[PF][SL];
-  auto gload = [&](uint4(&sr)[SL], int kb) {
-    const int soff_k = kb * BKV * (int)p.k_ss * 2, soff_v = kb * BKV * (int)p.v_ss * 2;
-    if (k_stager) {
-#pragma unroll
-      for (int i = 0; i < KL; ++i) {
-        const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
-        sr[i] = buf_load16(kres, (row * (int)p.k_ss + ch * 8) * 2, soff_k);
-      }
-    }
-    if (v_stager) {
-#pragma unroll
-      for (int i = 0; i < VL; ++i) {
-        const int blk = vtid + i * VTH;
-        const int kg = blk & 15, dc = blk >> 4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          // d >= D rows of V^T only feed O^T rows that are never written: no zeroing
-          sr[VOFF + 4 * i + r] = buf_load16(vres, ((4 * kg + r) * (int)p.v_ss + dc * 8) * 2, soff_v);
-        }
-      }
-    }
-  };
-  auto lstore = [&](const uint4(&sr)[SL], int stg) {
-    uint8_t* sK = smem + stg * STAGE;
-    uint8_t* sV = sK + KBYTES;
-    if (k_stager) {
-      // K columns d >= D (the next row's values when D < DP) meet zero Q columns,
-      // but must be zero themselves so that no inf or nan there reaches S
-      const bool kpad = p.D < DP;
-#pragma unroll
-      for (int i = 0; i < KL; ++i) {
-        const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
-        uint4 v = sr[i];
-        if (kpad) v = ch * 8 < p.D ? v : make_uint4(0, 0, 0, 0);
-        *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, ch)) = cvt_bf16x8_f16x8(v, sk);
-      }
-    }
-    if (v_stager) {
-#pragma unroll
-      for (int i = 0; i < VL; ++i) {
-        const int blk = vtid + i * VTH;
-        if (blk >= VBLK) continue;
-        const int kg = blk & 15, dc = blk >> 4;
-        uint4 cv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) cv[r] = cvt_bf16x8_f16x8(sr[VOFF + 4 * i + r], sv);
-        const int pos = perm16(4 * kg);  // 4 consecutive keys stay consecutive
-        const int chunk = pos >> 3, half_off = (pos & 7) * 2;
-        const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
-        const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
-        const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&cv[2]);
-        const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const uint2 g = gather4(w0[j >> 1], w1[j >> 1], w2[j >> 1], w3[j >> 1], j & 1);
-          *reinterpret_cast<uint2*>(sV + swz_vt(dc * 8 + j, chunk) + half_off) = g;
-        }
-      }
-    }
-  };
-
-  floatx16 acc_o[DB];
-#pragma unroll
-  for (int i = 0; i < DB; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc_o[i][r] = 0.f;
-  // running max in log2 units; stays stale until a row's max grows by more than
-  // 2^8, so exp2 arguments are <= 8 and P <= 256 (fp16-safe)
-  float m_run = -INFINITY, l_run = 0.f;
-  const float c = HAS_BIAS ? 1.f : p.scale_log2;
-
-  const int nkb_all = (p.Sk + BKV - 1) / BKV;
-  int nkb = nkb_all;
-  if constexpr (CAUSAL) nkb = min(nkb_all, (min(q0 + BQW, p.Sq) + BKV - 1) / BKV);
-  const uint16_t* brow = nullptr;
-  if constexpr (HAS_BIAS)
-    brow = p.bias + (int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh + (int64_t)min(qrow, p.Sq - 1) * p.bias_sq;
-
-  auto step = [&](int kb) {
-    const uint8_t* sK = smem + (kb & 1) * STAGE;
-    const uint8_t* sV = sK + KBYTES;
-    // S^T = K Q^T for two 32-key halves: lane = one query row, 16 keys each
-    floatx16 sacc[2];
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kh][r] = 0.f;
-#pragma unroll
+  // Query tiles of this block: one, or with pair (causal) the heavy tile
+  // ntiles-1-x and then the light tile x, so every block does the same work.
+  const int ntiles = (p.Sq + BQW - 1) / BQW;
+  const int bx = (int)blockIdx.x;
+  const int npass = (CAUSAL && p.pair) ? (bx == ntiles - 1 - bx ? 1 : 2) : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int qt = !CAUSAL ? bx : p.pair ? (pass == 0 ? ntiles - 1 - bx : bx) : (int)gridDim.x - 1 - bx;
+    const int q0 = qt * BQW;
+    // ---- Q fragments in registers (fp16, scaled by 2^a) ----
+    const int qrow = q0 + wave * 32 + fr;
+    half8 qf[KS];
+    {
+      const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)min(qrow, p.Sq - 1) * p.q_ss;
+  #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const half8 kf = *reinterpret_cast<const half8*>(sK + swz_k<DP>(kh * 32 + fr, 2 * s + fk));
-        sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[kh], 0, 0, 0);
+        const int d = 16 * s + 8 * fk;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (qrow < p.Sq && d < p.D) v = cvt_bf16x8_f16x8(ldg16(qp + d), sq);
+        qf[s] = __builtin_bit_cast(half8, v);
       }
     }
-    const int key0 = kb * BKV;
-    const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0 + wave * 32);
-    if constexpr (HAS_BIAS) {
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = key0 + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-          sacc[kh][r] = sacc[kh][r] * p.scale_log2 +
-                        (key < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[key]) * kLog2e : 0.f);
-        }
-    }
-    if (edge) mask_tile(sacc, key0, p.Sk, CAUSAL ? qrow : INT_MAX, fk);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kh][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
-    if (__any(mx > m_run + 8.f)) {  // wave-uniform: rescale O and l only when some row needs it
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < DB; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
-    }
-    const float mneg = (m_run == -INFINITY) ? 0.f : -m_run;
-    // row sums from the fp16 P that the PV product uses (v_dot2 with ones)
-    const half2v ones = {(_Float16)1.f, (_Float16)1.f};
-    float lsum = 0.f;
-    uint32_t pk[2][8];
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r], c, mneg));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r + 1], c, mneg));
-        pk[kh][r >> 1] = pack_f16(p0, p1);
-        lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pk[kh][r >> 1]), ones, lsum, false);
-      }
-    l_run += lsum;
-    // O^T += V^T P^T over four 16-key steps
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const uint4 pw = make_uint4(pk[ks >> 1][4 * (ks & 1) + 0], pk[ks >> 1][4 * (ks & 1) + 1],
-                                  pk[ks >> 1][4 * (ks & 1) + 2], pk[ks >> 1][4 * (ks & 1) + 3]);
-      const half8 pf = __builtin_bit_cast(half8, pw);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const half8 vf = *reinterpret_cast<const half8*>(sV + swz_vt(db * 32 + fr, 2 * ks + fk));
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc_o[db], 0, 0, 0);
-      }
-    }
-  };
 
-  // Pipeline as in the GEMM: LDS stage kb % 2 holds tile kb, register set u holds
-  // the tile congruent to u mod PF; the steady state issues its loads
-  // unconditionally so the younger sets stay in flight.
-#pragma unroll
-  for (int i = 0; i < PF; ++i)
-    if (i < nkb) gload(st[i], i);
-  if (nkb > 0) lstore(st[0], 0);
-  __syncthreads();
-  int kb0 = 0;
-  for (; kb0 + 2 * PF - 1 < nkb; kb0 += PF) {
-#pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      gload(st[u], kb0 + u + PF);
-      step(kb0 + u);
-      lstore(st[(u + 1) % PF], (kb0 + u + 1) & 1);
-      __syncthreads();
-    }
-  }
-  for (; kb0 < nkb; kb0 += PF) {
-#pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int kb = kb0 + u;
-      if (kb < nkb) {
-        if (kb + PF < nkb) gload(st[u], kb + PF);
-        step(kb);
-        if (kb + 1 < nkb) lstore(st[(u + 1) % PF], (kb + 1) & 1);
+    // ---- K / V staging through buffer loads (rows past Sk load as zeros) ----
+    const BufRes kres = make_res(p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh,
+                                 min<int64_t>((int64_t)p.Sk * p.k_ss * 2, 0x7fffffff));
+    const BufRes vres = make_res(p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh,
+                                 min<int64_t>((int64_t)p.Sk * p.v_ss * 2, 0x7fffffff));
+    const bool k_stager = NW != 8 || tid < KTH;
+    const bool v_stager = NW != 8 || tid >= VT0;
+    const int ktid = NW == 8 ? tid : tid, vtid = tid - VT0;
+    uint4 st[PF][SL];
+    auto gload = [&](uint4(&sr)[SL], int kb) {
+      const int soff_k = kb * BKV * (int)p.k_ss * 2, soff_v = kb * BKV * (int)p.v_ss * 2;
+      if (k_stager) {
+  #pragma unroll
+        for (int i = 0; i < KL; ++i) {
+          const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
+          sr[i] = buf_load16(kres, (row * (int)p.k_ss + ch * 8) * 2, soff_k);
+        }
+      }
+      if (v_stager) {
+  #pragma unroll
+        for (int i = 0; i < VL; ++i) {
+          const int blk = vtid + i * VTH;
+          const int kg = blk & 15, dc = blk >> 4;
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            // d >= D rows of V^T only feed O^T rows that are never written: no zeroing
+            sr[VOFF + 4 * i + r] = buf_load16(vres, ((4 * kg + r) * (int)p.v_ss + dc * 8) * 2, soff_v);
+          }
+        }
+      }
+    };
+    auto lstore = [&](const uint4(&sr)[SL], int stg) {
+      uint8_t* sK = smem + stg * STAGE;
+      uint8_t* sV = sK + KBYTES;
+      if (k_stager) {
+        // K columns d >= D (the next row's values when D < DP) meet zero Q columns,
+        // but must be zero themselves so that no inf or nan there reaches S
+        const bool kpad = p.D < DP;
+  #pragma unroll
+        for (int i = 0; i < KL; ++i) {
+          const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
+          uint4 v = sr[i];
+          if (kpad) v = ch * 8 < p.D ? v : make_uint4(0, 0, 0, 0);
+          *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, ch)) = cvt_bf16x8_f16x8(v, sk);
+        }
+      }
+      if (v_stager) {
+  #pragma unroll
+        for (int i = 0; i < VL; ++i) {
+          const int blk = vtid + i * VTH;
+          if (blk >= VBLK) continue;
+          const int kg = blk & 15, dc = blk >> 4;
+          uint4 cv[4];
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) cv[r] = cvt_bf16x8_f16x8(sr[VOFF + 4 * i + r], sv);
+          const int pos = perm16(4 * kg);  // 4 consecutive keys stay consecutive
+          const int chunk = pos >> 3, half_off = (pos & 7) * 2;
+          const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
+          const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
+          const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&cv[2]);
+          const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
+  #pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint2 g = gather4(w0[j >> 1], w1[j >> 1], w2[j >> 1], w3[j >> 1], j & 1);
+            *reinterpret_cast<uint2*>(sV + swz_vt(dc * 8 + j, chunk) + half_off) = g;
+          }
+        }
+      }
+    };
+
+    floatx16 acc_o[DB];
+  #pragma unroll
+    for (int i = 0; i < DB; ++i)
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) acc_o[i][r] = 0.f;
+    // running max in log2 units; stays stale until a row's max grows by more than
+    // 2^8, so exp2 arguments are <= 8 and P <= 256 (fp16-safe)
+    float m_run = -INFINITY, l_run = 0.f;
+    const float c = HAS_BIAS ? 1.f : p.scale_log2;
+
+    const int nkb_all = (p.Sk + BKV - 1) / BKV;
+    int nkb = nkb_all;
+    if constexpr (CAUSAL) nkb = min(nkb_all, (min(q0 + BQW, p.Sq) + BKV - 1) / BKV);
+    const uint16_t* brow = nullptr;
+    if constexpr (HAS_BIAS)
+      brow = p.bias + (int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh + (int64_t)min(qrow, p.Sq - 1) * p.bias_sq;
+
+    auto step = [&](int kb) {
+      const uint8_t* sK = smem + (kb & 1) * STAGE;
+      const uint8_t* sV = sK + KBYTES;
+      // S^T = K Q^T for two 32-key halves: lane = one query row, 16 keys each
+      floatx16 sacc[2];
+  #pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kh][r] = 0.f;
+  #pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const half8 kf = *reinterpret_cast<const half8*>(sK + swz_k<DP>(kh * 32 + fr, 2 * s + fk));
+          sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[kh], 0, 0, 0);
+        }
+      }
+      const int key0 = kb * BKV;
+      const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0 + wave * 32);
+      if constexpr (HAS_BIAS) {
+  #pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = key0 + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+            sacc[kh][r] = sacc[kh][r] * p.scale_log2 +
+                          (key < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[key]) * kLog2e : 0.f);
+          }
+      }
+      if (edge) mask_tile(sacc, key0, p.Sk, CAUSAL ? qrow : INT_MAX, fk);
+      float mx = -INFINITY;
+  #pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kh][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+      if (__any(mx > m_run + 8.f)) {  // wave-uniform: rescale O and l only when some row needs it
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+  #pragma unroll
+        for (int i = 0; i < DB; ++i)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
+      }
+      const float mneg = (m_run == -INFINITY) ? 0.f : -m_run;
+      // row sums from the fp16 P that the PV product uses (v_dot2 with ones)
+      const half2v ones = {(_Float16)1.f, (_Float16)1.f};
+      float lsum = 0.f;
+      uint32_t pk[2][8];
+  #pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+  #pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r], c, mneg));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r + 1], c, mneg));
+          pk[kh][r >> 1] = pack_f16(p0, p1);
+          lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pk[kh][r >> 1]), ones, lsum, false);
+        }
+      l_run += lsum;
+      // O^T += V^T P^T over four 16-key steps
+  #pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const uint4 pw = make_uint4(pk[ks >> 1][4 * (ks & 1) + 0], pk[ks >> 1][4 * (ks & 1) + 1],
+                                    pk[ks >> 1][4 * (ks & 1) + 2], pk[ks >> 1][4 * (ks & 1) + 3]);
+        const half8 pf = __builtin_bit_cast(half8, pw);
+  #pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const half8 vf = *reinterpret_cast<const half8*>(sV + swz_vt(db * 32 + fr, 2 * ks + fk));
+          acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc_o[db], 0, 0, 0);
+        }
+      }
+    };
+
+    // Pipeline as in the GEMM: LDS stage kb % 2 holds tile kb, register set u holds
+    // the tile congruent to u mod PF; the steady state issues its loads
+    // unconditionally so the younger sets stay in flight.
+  #pragma unroll
+    for (int i = 0; i < PF; ++i)
+      if (i < nkb) gload(st[i], i);
+    if (nkb > 0) lstore(st[0], 0);
+    __syncthreads();
+    int kb0 = 0;
+    for (; kb0 + 2 * PF - 1 < nkb; kb0 += PF) {
+  #pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        gload(st[u], kb0 + u + PF);
+        step(kb0 + u);
+        lstore(st[(u + 1) % PF], (kb0 + u + 1) & 1);
         __syncthreads();
       }
     }
-  }
-
-  // ---- epilogue ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (qrow >= p.Sq) return;
-  const float sev = ldexp1(ev);
-  const int64_t orow = ((int64_t)bh * p.Sq + qrow) * p.D;
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      const int d = db * 32 + 8 * rq + 4 * fk;
-      if (d >= p.D) continue;
-      float y[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = l_tot > 0.f ? acc_o[db][4 * rq + e] / l_tot : 0.f;
-      *reinterpret_cast<uint2*>(p.o + orow + d) =
-          make_uint2(pack_bf16(y[0] * sev, y[1] * sev), pack_bf16(y[2] * sev, y[3] * sev));
-      if (p.o16) *reinterpret_cast<uint2*>(p.o16 + orow + d) = make_uint2(pack_f16(y[0], y[1]), pack_f16(y[2], y[3]));
+    for (; kb0 < nkb; kb0 += PF) {
+  #pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int kb = kb0 + u;
+        if (kb < nkb) {
+          if (kb + PF < nkb) gload(st[u], kb + PF);
+          step(kb);
+          if (kb + 1 < nkb) lstore(st[(u + 1) % PF], (kb + 1) & 1);
+          __syncthreads();
+        }
+      }
     }
-  // lse in log2 units (v_log_f32); rows that see no key get +inf so the
-  // backward's exp2(logit - lse) is 0 there
-  if (p.lse && fk == 0)
-    p.lse[(int64_t)bh * p.Sq + qrow] = (l_tot > 0.f) ? m_run + __builtin_amdgcn_logf(l_tot) : INFINITY;
+
+    // ---- epilogue ----
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    if (qrow < p.Sq) {
+    const float sev = ldexp1(ev);
+    const int64_t orow = ((int64_t)bh * p.Sq + qrow) * p.D;
+  #pragma unroll
+    for (int db = 0; db < DB; ++db)
+  #pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = db * 32 + 8 * rq + 4 * fk;
+        if (d >= p.D) continue;
+        float y[4];
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = l_tot > 0.f ? acc_o[db][4 * rq + e] / l_tot : 0.f;
+        *reinterpret_cast<uint2*>(p.o + orow + d) =
+            make_uint2(pack_bf16(y[0] * sev, y[1] * sev), pack_bf16(y[2] * sev, y[3] * sev));
+        if (p.o16) *reinterpret_cast<uint2*>(p.o16 + orow + d) = make_uint2(pack_f16(y[0], y[1]), pack_f16(y[2], y[3]));
+      }
+    // lse in log2 units (v_log_f32); rows that see no key get +inf so the
+    // backward's exp2(logit - lse) is 0 there
+    if (p.lse && fk == 0)
+      p.lse[(int64_t)bh * p.Sq + qrow] = (l_tot > 0.f) ? m_run + __builtin_amdgcn_logf(l_tot) : INFINITY;
+    }
+  }
 }
 
 struct WsLayout {
@@ -439,14 +449,22 @@ int launch_fwd_nw(const FwdParams& p, bool causal, bool has_bias, dim3 grid, hip
 // S = 16384 (1024 blocks). Head dim 256 always uses 4-wave blocks (one wave per
 // SIMD, 512 registers).
 template <int DP>
-int launch_fwd_dp(const FwdParams& p, bool causal, bool has_bias, hipStream_t st, int nw_override) {
-  const int64_t tiles8 = cdiv(p.Sq, 256) * p.B * p.H;
-  int nw = nw_override > 0 ? nw_override : (tiles8 >= 128 && tiles8 < 1024 ? 8 : 4);
+int launch_fwd_dp(FwdParams p, bool causal, bool has_bias, hipStream_t st, int nw_override) {
+  const int64_t tiles8 = cdiv(p.Sq, 256) * p.B * p.H, tiles4 = cdiv(p.Sq, 128) * p.B * p.H;
+  // causal with at most ~4 blocks per CU: 4-wave blocks that pair a heavy and a
+  // light query tile, so every block has the same work (heaviest-first ordering
+  // only balances many rounds); otherwise as measured above
+  const bool pair = causal && tiles4 >= 2 * p.B * p.H && tiles4 <= 1024 && nw_override <= 0 &&
+                    getenv("TBF16_ATTN_NOPAIR") == nullptr;
+  int nw = nw_override > 0 ? nw_override : pair ? 4 : (tiles8 >= 128 && tiles8 < 1024 ? 8 : 4);
   if (DP > 128) nw = 4;
+  const int64_t ntiles = cdiv(p.Sq, nw == 8 ? 256 : 128);
+  p.pair = pair && nw == 4;
+  const dim3 grid((unsigned)(p.pair ? cdiv(ntiles, 2) : ntiles), p.B * p.H);
   if (nw == 8) {
-    if constexpr (DP <= 128) return launch_fwd_nw<DP, 8, 2>(p, causal, has_bias, dim3((unsigned)cdiv(p.Sq, 256), p.B * p.H), st);
+    if constexpr (DP <= 128) return launch_fwd_nw<DP, 8, 2>(p, causal, has_bias, grid, st);
   }
-  return launch_fwd_nw<DP, 4, 1>(p, causal, has_bias, dim3((unsigned)cdiv(p.Sq, 128), p.B * p.H), st);
+  return launch_fwd_nw<DP, 4, 1>(p, causal, has_bias, grid, st);
 }
 
 int check_bhsd(const char* fn, const char* name, const void* x, const int64_t* st, int64_t D) {
@@ -515,6 +533,7 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   p.lse = lse;
   p.o16 = (uint16_t*)o16;
   p.exps = exps;
+  p.pair = 0;
   const char* ov = getenv("TBF16_ATTN_WAVES");  // benchmarking override: 4 or 8
   const int nw = ov ? atoi(ov) : 0;
   if (D <= 64) return launch_fwd_dp<64>(p, causal != 0, bias != nullptr, st, nw);
