@@ -15,11 +15,17 @@
 //    fragment reads (ds_read_b128) and the row stores are bank-conflict free.
 //  - PF register sets are in flight: each k tile's global loads are issued PF
 //    compute phases before they are stored to LDS.
-//  - the headline shape uses three LDS stages in a ring with fragments read
-//    one 16-wide k step ahead of the MFMAs (the next tile's first step
-//    included), one barrier per k tile, and an instruction-group schedule that
-//    spreads a k step's LDS reads, A conversions, LDS writes and global loads
-//    between its MFMAs; the two-stage form is kept for the smaller tiles.
+//  - the headline shape (config 9) uses BK = 64, so that every global load
+//    instruction covers whole 128-byte row segments: half the L2 requests of
+//    BK = 32, which measurably raises the clock the chip holds under this
+//    kernel. Two LDS stages of 64 KB; fragments are read one 16-wide k step
+//    ahead of the MFMAs and the last k step of each tile runs after the tile's
+//    barrier, covering the latency of the next tile's first LDS reads. An
+//    instruction-group schedule spreads each step's LDS reads, A conversions,
+//    LDS writes and global loads between its MFMAs.
+//  - config 0 (BK = 32, three LDS stages in a ring, the next tile's first
+//    fragments read before the barrier) and the plain two-stage loop of the
+//    smaller tiles remain selectable.
 //  - the MFMA's first operand is the b fragment, the second the a fragment, so a
 //    lane's 16 accumulators are four runs of 4 consecutive n for one m. The
 //    epilogue rounds once to bf16, stages the tile rows in LDS and writes each
@@ -71,7 +77,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   constexpr int PFIT = (BM * PITCH <= 2 * STAGE) ? 1 : (BM / 2 * PITCH <= 2 * STAGE) ? 2 : 4;
   constexpr int PASSES = PFIT < BM / TM ? PFIT : BM / TM;
   constexpr int RPP = BM / PASSES;
-  constexpr int NSTG = NS >= 3 ? 3 : 2;  // LDS stages
+  constexpr int NSTG = NS == 5 ? 2 : NS >= 3 ? 3 : 2;  // LDS stages
   constexpr bool SCHED = NS == 4;
   constexpr int SMEM = NSTG * STAGE > RPP * PITCH ? NSTG * STAGE : RPP * PITCH;
   __shared__ __align__(16) uint8_t smem[SMEM];
@@ -199,6 +205,122 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
         }
       }
     }
+  } else if constexpr (NS == 5) {
+    // Two LDS stages of BK = 64 (whole 128-byte row segments per global load) and
+    // the last k step of every tile deferred past the tile's barrier: after the
+    // barrier a wave issues the LDS reads of the next tile's first step and then
+    // the deferred step's MFMAs, whose fragments it read before the barrier, so the
+    // read latency hides behind them. Tile kt + 1 is stored (A in step 0, B in
+    // step 1) into the stage freed by the previous barrier and the loads of tile
+    // kt + 1 + PF go out into the register set just emptied.
+    constexpr int SUB = BK / 16;
+    static_assert(SUB == 4, "deferred-step loop assumes four k steps per tile");
+    half8 fb[2][FN], fa[2][FM];
+    auto fread = [&](half8(&bf)[FN], half8(&af)[FM], int stg, int s) {
+      const uint8_t* sA = smem + stg * STAGE;
+      const uint8_t* sB = sA + BM * RB;
+      const int c = 2 * s + fk;
+#pragma unroll
+      for (int i = 0; i < FN; ++i) bf[i] = *reinterpret_cast<const half8*>(sB + swz<BK>(wn * TN + i * 32 + fr, c));
+#pragma unroll
+      for (int j = 0; j < FM; ++j) af[j] = *reinterpret_cast<const half8*>(sA + swz<BK>(wm * TM + j * 32 + fr, c));
+    };
+    auto mma = [&](const half8(&bf)[FN], const half8(&af)[FM]) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[i], af[j], acc[i][j], 0, 0, 0);
+    };
+    // staging in three parts: A rows [0, AL/2) in step 0, [AL/2, AL) in step 1,
+    // B in step 2 (part q covers register slots [lo, hi) of one operand)
+    static_assert(AL % 2 == 0, "A staging splits in halves");
+    auto stage_part = [&](int q, const uint4(&va)[AL], const uint4(&vb)[BL], int stg) {
+      uint8_t* sA = smem + stg * STAGE;
+      uint8_t* sB = sA + BM * RB;
+      if (q < 2) {
+#pragma unroll
+        for (int i = q * AL / 2; i < (q + 1) * AL / 2; ++i) {
+          uint4 v = va[i];
+          if constexpr (A_BF16) v = cvt_bf16x8_f16x8(v, as[i]);
+          *reinterpret_cast<uint4*>(sA + swz<BK>(lrow + i * RP, lch)) = v;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < BL; ++i) *reinterpret_cast<uint4*>(sB + swz<BK>(lrow + i * RP, lch)) = vb[i];
+      }
+    };
+    auto load_part = [&](int q, uint4(&va)[AL], uint4(&vb)[BL], int kt) {
+      const int koff = kt * BK * 2;
+      const bool kok = EVEN || kt * BK + lch * 8 < K;
+      if (q < 2) {
+#pragma unroll
+        for (int i = q * AL / 2; i < (q + 1) * AL / 2; ++i) {
+          const uint4 v = buf_load16(arsrc, aoff[i], koff);
+          va[i] = kok ? v : make_uint4(0, 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < BL; ++i) {
+          const uint4 v = buf_load16(brsrc, boff[i], koff);
+          vb[i] = kok ? v : make_uint4(0, 0, 0, 0);
+        }
+      }
+    };
+    constexpr int MF = FN * FM, RD = FN + FM;
+    constexpr int VT = A_BF16 ? 10 * AL : 0;  // VALU ops of converting half of a thread's A slots
+    // instruction groups of one k step: the next step's reads first (two per
+    // MFMA), then each MFMA followed by its share of the staging work
+    auto sched = [&](int part, bool store, bool load, bool reads) {
+      const int n = part < 0 ? 0 : part < 2 ? AL / 2 : BL;
+#pragma unroll
+      for (int i = 0; i < MF; ++i) {
+        if (reads && 2 * i < RD) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (VT && store && part >= 0 && part < 2) __builtin_amdgcn_sched_group_barrier(0x002, (VT + MF - 1) / MF, 0);
+        if (store && i >= MF - n) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+        if (load && i >= MF - n) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // one tile: the deferred step of tile kt - 1 (if any), steps 0 .. SUB - 2 of
+    // tile kt, staging of tile kt + 1 from set v and loads of tile kt + 1 + PF
+    auto tile = [&](int kt, int v, bool deferred, bool store, bool load) {
+      const int stg = kt & 1;
+      fread(fb[0], fa[0], stg, 0);
+      if (deferred) {
+        mma(fb[1], fa[1]);
+        sched(-1, false, false, false);
+      }
+#pragma unroll
+      for (int s = 0; s < SUB - 1; ++s) {
+        fread(fb[(s + 1) & 1], fa[(s + 1) & 1], stg, s + 1);
+        if (store) stage_part(s, ra[v], rb[v], stg ^ 1);
+        if (load) load_part(s, ra[v], rb[v], kt + 1 + PF);
+        mma(fb[s & 1], fa[s & 1]);
+        sched(s, store, load, true);
+      }
+      __syncthreads();
+    };
+    // prologue: tile 0 stored, tiles 1 .. PF in flight (tile j in set j % PF)
+#pragma unroll
+    for (int q = 0; q < PF; ++q)
+      if (q < KT) gload(ra[q], rb[q], q);
+    lstore(ra[0], rb[0], 0);
+    if (PF < KT) gload(ra[0], rb[0], PF);
+    __syncthreads();
+    int kt0 = 0;
+    for (; kt0 + 1 + PF + PF - 1 < KT; kt0 += PF) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) tile(kt0 + u, (u + 1) % PF, kt0 + u > 0, true, true);
+    }
+    for (; kt0 < KT; kt0 += PF) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int kt = kt0 + u;
+        if (kt < KT) tile(kt, (u + 1) % PF, kt > 0, kt + 1 < KT, kt + 1 + PF < KT);
+      }
+    }
+    mma(fb[1], fa[1]);  // the last tile's deferred step
   } else {
     // Three LDS stages in a ring (tile kt in stage kt % 3) and fragments read one
     // 16-wide k step ahead of the MFMAs that use them, the next tile's first step
@@ -553,8 +675,9 @@ struct TileCfg {
 // 7: M <= 64, as 6 with 3 chunks in flight
 // 8: M <= 64, 64 b rows per block, as 6 with 2 chunks in flight
 constexpr TileCfg kCfgs[] = {{256, 256, 32}, {128, 128, 64}, {64, 64, 64},       {128, 128, 64},    {256, 256, 32},
-                             {32, 32, 64, true}, {32, 32, 64, true}, {64, 32, 64, true}, {64, 64, 64, true}};
-constexpr int kNumCfgs = 9;
+                             {32, 32, 64, true}, {32, 32, 64, true}, {64, 32, 64, true}, {64, 64, 64, true},
+                             {256, 256, 64}};
+constexpr int kNumCfgs = 10;
 
 // Measured on MI355X (4096^3; 8192x6144x2048; decode K = 2560, N = 10240):
 // the grouped-schedule 256x256 tile wherever it fills the chip, the 64-row
@@ -565,7 +688,7 @@ int pick_cfg(int64_t M, int64_t N) {
     if (cdiv(N, 64) >= 160) return 8;
     return M <= 32 ? 6 : 7;
   }
-  if (tiles(0) >= 128) return 0;
+  if (tiles(9) >= 128) return 9;
   if (tiles(1) >= 256) return 1;
   if (tiles(3) >= 128) return 3;
   return 2;
@@ -605,6 +728,7 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
     case 2: CFG(64, 64, 2, 2, 64, 2, 2); break;
     case 3: CFG(128, 128, 2, 2, 64, 2, 3); break;
     case 4: CFG(256, 256, 4, 2, 32, 3, 2); break;
+    case 9: CFG(256, 256, 4, 2, 64, 1, 5); break;
 #define SKINNY(NB_, MB_, NW_, PF_, TR_)                                                                         \
   skinny_kernel<NB_, MB_, NW_, PF_, TR_, A_BF16><<<g, NW_ * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, \
                                                                         ldc, M, N, K)
