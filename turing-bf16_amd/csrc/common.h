@@ -92,6 +92,40 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// amax (or L1 norm) of a bf16 row, reduced over the wave; valid in every lane.
+// L1 accumulates in fp64 and rounds once to fp32, so the exponent is that of the
+// exact sum (the reference's fp32 thread-order sum, small_kernels.cu:42-59, can
+// differ only within one fp32 ulp of a power of two).
+__device__ __forceinline__ float row_amax_wave(const uint16_t* xr, int K, int lane, bool l1) {
+  const uint4* p = reinterpret_cast<const uint4*>(xr);
+  const int K8 = K >> 3;
+  if (l1) {
+    double acc = 0.0;
+    for (int i = lane; i < K8; i += kWave) {
+      uint4 v = p[i];
+      acc += (double)fabsf(bf16_lo(v.x)) + (double)fabsf(bf16_hi(v.x)) + (double)fabsf(bf16_lo(v.y)) +
+             (double)fabsf(bf16_hi(v.y)) + (double)fabsf(bf16_lo(v.z)) + (double)fabsf(bf16_hi(v.z)) +
+             (double)fabsf(bf16_lo(v.w)) + (double)fabsf(bf16_hi(v.w));
+    }
+    return (float)wave_sum_d(acc);
+  }
+  float m0 = 0.f, m1 = 0.f;
+  int i = lane;
+  for (; i + kWave < K8; i += 2 * kWave) {
+    uint4 a = p[i], b = p[i + kWave];
+    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.x)), fabsf(bf16_hi(a.x))), fmaxf(fabsf(bf16_lo(a.y)), fabsf(bf16_hi(a.y)))));
+    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.z)), fabsf(bf16_hi(a.z))), fmaxf(fabsf(bf16_lo(a.w)), fabsf(bf16_hi(a.w)))));
+    m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(bf16_lo(b.x)), fabsf(bf16_hi(b.x))), fmaxf(fabsf(bf16_lo(b.y)), fabsf(bf16_hi(b.y)))));
+    m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(bf16_lo(b.z)), fabsf(bf16_hi(b.z))), fmaxf(fabsf(bf16_lo(b.w)), fabsf(bf16_hi(b.w)))));
+  }
+  if (i < K8) {
+    uint4 a = p[i];
+    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.x)), fabsf(bf16_hi(a.x))), fmaxf(fabsf(bf16_lo(a.y)), fabsf(bf16_hi(a.y)))));
+    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.z)), fabsf(bf16_hi(a.z))), fmaxf(fabsf(bf16_lo(a.w)), fabsf(bf16_hi(a.w)))));
+  }
+  return wave_max(fmaxf(m0, m1));
+}
+
 // ---- memory ------------------------------------------------------------------
 
 typedef int int4v __attribute__((ext_vector_type(4)));

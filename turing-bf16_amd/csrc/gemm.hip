@@ -55,7 +55,7 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   else return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int PF, int NS, bool A_BF16, bool EVEN>
+template <int BM, int BN, int WM, int WN, int BK, int PF, int NS, bool A_BF16, bool KEVEN>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                            const int32_t* __restrict__ a_exp,
                                                            const float* __restrict__ a_sinv,
@@ -101,7 +101,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   // offsets (VGPRs) and the k offset in an SGPR: no per-iteration address math
   // in vector registers, so in-flight loads of other register sets are never
   // waited for early. Rows past M (N) lie past the resource's end and load as
-  // zeros; a K tail (K % BK != 0) is zeroed by a select.
+  // zeros; a K tail (K % BK != 0) is zeroed by a select, compiled in only when
+  // KEVEN is false (a select on a loaded value makes the compiler wait for that
+  // load on the spot, which serialises the register pipeline).
   const int lrow = tid / CPR, lch = tid % CPR;
   const BufRes arsrc = make_res(A + (int64_t)m0 * lda, min<int64_t>((int64_t)(M - m0) * lda * 2, 0x7fffffff));
   const BufRes brsrc = make_res(B + (int64_t)n0 * ldb, min<int64_t>((int64_t)(N - n0) * ldb * 2, 0x7fffffff));
@@ -111,14 +113,14 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   for (int i = 0; i < AL; ++i) {
     const int r = lrow + i * RP;
     aoff[i] = (r * (int)lda + lch * 8) * 2;
-    if constexpr (A_BF16) as[i] = (EVEN || m0 + r < M) ? pow2f(a_exp[m0 + r]) : 0.f;
+    if constexpr (A_BF16) as[i] = m0 + r < M ? pow2f(a_exp[m0 + r]) : 0.f;
   }
 #pragma unroll
   for (int i = 0; i < BL; ++i) boff[i] = ((lrow + i * RP) * (int)ldb + lch * 8) * 2;
   uint4 ra[PF][AL], rb[PF][BL];
   auto gload = [&](uint4(&va)[AL], uint4(&vb)[BL], int kt) {
     const int koff = kt * BK * 2;
-    const bool kok = EVEN || kt * BK + lch * 8 < K;
+    const bool kok = KEVEN || kt * BK + lch * 8 < K;
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
       const uint4 v = buf_load16(arsrc, aoff[i], koff);
@@ -251,7 +253,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
     };
     auto load_part = [&](int q, uint4(&va)[AL], uint4(&vb)[BL], int kt) {
       const int koff = kt * BK * 2;
-      const bool kok = EVEN || kt * BK + lch * 8 < K;
+      const bool kok = KEVEN || kt * BK + lch * 8 < K;
       if (q < 2) {
 #pragma unroll
         for (int i = q * AL / 2; i < (q + 1) * AL / 2; ++i) {
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
         const int ml = wm * TM + j * 32 + fr;  // row within the tile
         const int m = m0 + ml;
         float sa = 0.f;
-        if (EVEN || m < M) {
+        if (m < M) {
           if constexpr (A_BF16) sa = ldexp1(-a_exp[m]);
           else sa = a_sinv[m];
         }
@@ -438,7 +440,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
             const int n = n0 + nl;
             float4 sb = make_float4(0.f, 0.f, 0.f, 0.f);
             float bb[4] = {0.f, 0.f, 0.f, 0.f};
-            if (EVEN || n < N) {
+            if (n < N) {
               sb = *reinterpret_cast<const float4*>(b_sinv + n);
               if (bias) {
                 const uint32_t b01 = *reinterpret_cast<const uint32_t*>(bias + n);
@@ -461,7 +463,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
     for (int c = tid; c < RPP * OCR; c += NT) {
       const int rl = c / OCR, cc = c % OCR;
       const int m = m0 + pass * RPP + rl, n = n0 + cc * 8;
-      if (EVEN || (m < M && n < N))
+      if (m < M && n < N)
         stg16(C + (int64_t)m * ldc + n, *reinterpret_cast<const uint4*>(smem + rl * PITCH + cc * 16));
     }
     if (PASSES > 1) __syncthreads();
@@ -674,24 +676,45 @@ struct TileCfg {
 // 6: M <= 32, b loaded coalesced and transposed through LDS, 4 chunks in flight
 // 7: M <= 64, as 6 with 3 chunks in flight
 // 8: M <= 64, 64 b rows per block, as 6 with 2 chunks in flight
+// Two-stage k 64 loop with the last k step deferred past the barrier:
+// 9: 256x256, 8 waves of 64x128, 1 set
+// 10: 256x128, 8 waves of 64x64, 1 set
+// 11: 256x64, 8 waves of 64x32, 2 sets
+// and 12: 128x64, 4 waves of 64x32, k 64, 3 sets, 3 stages
 constexpr TileCfg kCfgs[] = {{256, 256, 32}, {128, 128, 64}, {64, 64, 64},       {128, 128, 64},    {256, 256, 32},
                              {32, 32, 64, true}, {32, 32, 64, true}, {64, 32, 64, true}, {64, 64, 64, true},
-                             {256, 256, 64}};
-constexpr int kNumCfgs = 10;
+                             {256, 256, 64}, {256, 128, 64}, {256, 64, 64}, {128, 64, 64}};
+constexpr int kNumCfgs = 13;
 
-// Measured on MI355X (4096^3; 8192x6144x2048; decode K = 2560, N = 10240):
-// the grouped-schedule 256x256 tile wherever it fills the chip, the 64-row
-// skinny block for M <= 64 when there are enough b rows to keep 160 blocks busy.
+// Configuration choice, fitted to measurements on MI355X (256 CUs): for M <= 64
+// with enough b rows for 160 blocks, the 64-row skinny block up to M = 32 and
+// the LDS-staged 64x64 tile above (every skinny block re-reads all of a, which
+// costs more than the weights from M ~ 40 on). Otherwise the tile that maximises
+// eff x (blocks / whole rounds of 256 blocks) x (M / M rounded up to the tile):
+// larger tiles run faster per CU (eff), but a partial last round of blocks or a
+// mostly empty row of tiles wastes CUs.
 int pick_cfg(int64_t M, int64_t N) {
-  auto tiles = [&](int c) { return cdiv(M, kCfgs[c].bm) * cdiv(N, kCfgs[c].bn); };
   if (M <= 64) {
-    if (cdiv(N, 64) >= 160) return 8;
+    if (cdiv(N, 64) >= 160) return M <= 32 ? 8 : 2;
     return M <= 32 ? 6 : 7;
   }
-  if (tiles(9) >= 128) return 9;
-  if (tiles(1) >= 256) return 1;
-  if (tiles(3) >= 128) return 3;
-  return 2;
+  constexpr int64_t kCUs = 256;
+  constexpr int cand[] = {9, 10, 11, 12, 2};
+  constexpr float eff[] = {1.0f, 0.85f, 0.7f, 0.6f, 0.45f};
+  int best = 2;
+  float best_score = -1.f;
+  for (int i = 0; i < 5; ++i) {
+    const TileCfg& t = kCfgs[cand[i]];
+    const int64_t mt = cdiv(M, t.bm), tiles = mt * cdiv(N, t.bn);
+    const float util = (float)tiles / (float)(cdiv(tiles, kCUs) * kCUs);
+    const float mutil = (float)M / (float)(mt * t.bm);
+    const float score = eff[i] * util * mutil;
+    if (score > best_score) {
+      best_score = score;
+      best = cand[i];
+    }
+  }
+  return best;
 }
 
 template <int BM, int BN, int WM, int WN, int BK, int PF, int NS, bool A_BF16>
@@ -714,7 +737,7 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
   TB_CHECK(!kCfgs[cfg].skinny || M <= bm, "gemm: configuration %d takes M <= %d", cfg, bm);
   const int64_t blocks = kCfgs[cfg].skinny ? cdiv(N, bn) : cdiv(M, bm) * cdiv(N, bn);
   TB_CHECK(blocks < (int64_t)1 << 31, "gemm: grid too large");
-  const bool even = M % bm == 0 && N % bn == 0 && K % kCfgs[cfg].bk == 0;
+  const bool even = K % kCfgs[cfg].bk == 0;  // no k-tail selects on loaded values
   const auto a = (const uint16_t*)A;
   const auto b = (const uint16_t*)B;
   const auto bi = (const uint16_t*)bias;
@@ -729,6 +752,9 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
     case 3: CFG(128, 128, 2, 2, 64, 2, 3); break;
     case 4: CFG(256, 256, 4, 2, 32, 3, 2); break;
     case 9: CFG(256, 256, 4, 2, 64, 1, 5); break;
+    case 10: CFG(256, 128, 4, 2, 64, 1, 5); break;
+    case 11: CFG(256, 64, 4, 2, 64, 2, 5); break;
+    case 12: CFG(128, 64, 2, 2, 64, 3, 3); break;
 #define SKINNY(NB_, MB_, NW_, PF_, TR_)                                                                         \
   skinny_kernel<NB_, MB_, NW_, PF_, TR_, A_BF16><<<g, NW_ * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, \
                                                                         ldc, M, N, K)
