@@ -2,7 +2,9 @@
 //
 // Scaling (tbf16/autograd.py:166-193): e = max_{b,h}(frexp(amax dO[b,h]) + ev_q[b,h]),
 // G = t_do - e, dO16 = fp16(dO * 2^(ev_q + G)); with q16 = q 2^a, k16 = k 2^-a,
-// v16 = v 2^-ev converted on the fly from the bf16 inputs:
+// v16 = v 2^-ev (the workspace holds all four as zero-padded fp16 copies, rows to
+// a multiple of 128 and columns to DP, written by one conversion pass and by the
+// delta kernel, so the MFMA kernels stage plain fp16 with no conversion work):
 //   P = exp2(S * scale * log2e - lse), dP = dO16 V16^T, delta = rowsum(dO16 * O16),
 //   dS = P (dP - delta),
 //   dv = bf16(sum_q P^T dO16 * 2^(-ev-G)), dk = bf16(scale * sum_q dS^T Q16 * 2^(-a-G)),
@@ -13,7 +15,8 @@
 // with t_do - 8 (the reference's condition, tbf16/autograd.py:184-187).
 //
 // Kernels (4 waves, v_mfma_f32_32x32x16_f16):
-//   delta:   one 16-lane group per query row; also computes e, G.
+//   prep:    q16, k16, v16 (one launch, memory-bound); its first block derives e, G.
+//   delta:   one 16-lane group per query row; also writes dO16.
 //   dkdv:    block = 128 keys (32 per wave, K16 fragments in registers, V16 rows in
 //            per-wave LDS), loops over 64-query tiles (and over the query heads
 //            of a GQA group). Q and dO tiles sit in LDS row-major: the A operand
@@ -59,6 +62,9 @@ struct BwdParams {
   const float* part_do;
   int nch_do;
   float* delta;     // (B, H, Sq)
+  // zero-padded fp16 copies: (B, H, Sqp, DP) for q16 / do16, (B, Hkv, Skp, DP) for k16 / v16
+  uint16_t *q16, *k16, *v16, *do16;
+  int Sqp, Skp, DPc;
   int32_t* exps_out;  // {e, G}
   int32_t* overflow;
   uint16_t *dq, *dk, *dv;
@@ -87,24 +93,67 @@ __device__ int compute_e(const BwdParams& p, int* red) {
 
 __device__ __forceinline__ bool bad16(float x) { return !(fabsf(x) < kF16Overflow); }
 
-// ---- delta = rowsum(dO16 * O16), and {e, G} -----------------------------------
-__global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
+// ---- q16 = fp16(q 2^a), k16 = fp16(k 2^-a), v16 = fp16(v 2^-ev), and {e, G} -----
+// Grid: x = groups of 4 x 256 / (DP / 8) padded rows, y = (copy, batch, head) with the
+// q heads first, then the k and v heads. Zeros past the real rows and columns.
+// Block (0, 0) also derives e and G (they are needed by the delta pass only).
+__global__ __launch_bounds__(NTH) void prep_kernel(BwdParams p) {
   __shared__ int red[4];
-  const int e = compute_e(p, red);
-  const int G = p.t_do - e;
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
-    p.exps_out[0] = e;
-    p.exps_out[1] = G;
+  if (blockIdx.x == 0 && blockIdx.y == 0) {
+    const int e = compute_e(p, red);
+    if (threadIdx.x == 0) {
+      p.exps_out[0] = e;
+      p.exps_out[1] = p.t_do - e;
+    }
   }
+  const int CPR = p.DPc / 8;
+  const int nq = p.B * p.H, nk = p.B * p.Hkv;
+  const int y = blockIdx.y;
+  const int seg = y < nq ? 0 : y < nq + nk ? 1 : 2;
+  const int bh = seg == 0 ? y : seg == 1 ? y - nq : y - nq - nk;
+  const int HH = seg == 0 ? p.H : p.Hkv, b = bh / HH, h = bh % HH;
+  const int Sp = seg == 0 ? p.Sqp : p.Skp, S = seg == 0 ? p.Sq : p.Sk;
+  const int a = p.exps_fwd[0];
+  const int e = seg == 0 ? a : seg == 1 ? -a : -p.exps_fwd[2 + bh];
+  const float sc = ldexp1(e);
+  const uint16_t* src = seg == 0   ? p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh
+                        : seg == 1 ? p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh
+                                   : p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
+  const int64_t ss = seg == 0 ? p.q_ss : seg == 1 ? p.k_ss : p.v_ss;
+  uint16_t* dst = (seg == 0 ? p.q16 : seg == 1 ? p.k16 : p.v16) + (int64_t)bh * Sp * p.DPc;
+  // four rows per thread, all loads issued before the stores
+  const int rpb = NTH / CPR, ch = threadIdx.x % CPR;
+  const int row0 = blockIdx.x * 4 * rpb + threadIdx.x / CPR;
+  uint4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + i * rpb;
+    v[i] = row < S && ch * 8 < p.D ? ldg16(src + (int64_t)row * ss + ch * 8) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + i * rpb;
+    if (row < Sp) stg16(dst + (int64_t)row * p.DPc + ch * 8, cvt_bf16x8_f16x8(v[i], sc));
+  }
+}
+
+// ---- delta = rowsum(dO16 * O16), and dO16 ------------------------------------------
+// One 16-lane group per padded query row; G comes from the prep pass.
+__global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
+  const int G = p.exps_out[1];
   const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
   const float sdo = ldexp1(ev_of(p, b, h) + G);
   const int row = blockIdx.x * 16 + (threadIdx.x >> 4), l16 = threadIdx.x & 15;
   float acc = 0.f;
+  // dO16 row (zeros past Sq and past D), 8 columns per lane (DP <= 128)
+  uint16_t* wrow = p.do16 + ((int64_t)bh * p.Sqp + row) * p.DPc;
+  if (row < p.Sqp && l16 * 8 < p.DPc && (row >= p.Sq || l16 * 8 >= p.D)) stg16(wrow + l16 * 8, make_uint4(0, 0, 0, 0));
   if (row < p.Sq) {
     const uint16_t* dr = p.dout + (int64_t)b * p.d_sb + (int64_t)h * p.d_sh + (int64_t)row * p.d_ss;
     const uint16_t* orow = p.o16 + ((int64_t)bh * p.Sq + row) * p.D;
     for (int d = l16 * 8; d < p.D; d += 128) {
       const uint4 dv = cvt_bf16x8_f16x8(ldg16(dr + d), sdo);
+      stg16(wrow + d, dv);
       const uint4 ov = ldg16(orow + d);
       acc += f16_lo(dv.x) * f16_lo(ov.x) + f16_hi(dv.x) * f16_hi(ov.x) + f16_lo(dv.y) * f16_lo(ov.y) +
              f16_hi(dv.y) * f16_hi(ov.y) + f16_lo(dv.z) * f16_lo(ov.z) + f16_hi(dv.z) * f16_hi(ov.z) +
@@ -153,16 +202,14 @@ dkdv_kernel(BwdParams p) {
   half8 kf[KS];
   uint8_t* sVw = smem + wave * VW;
   {
-    const float sk = ldexp1(-a), sv = ldexp1(-ev);
-    const uint16_t* kr = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh + (int64_t)min(key, p.Sk - 1) * p.k_ss;
-    const uint16_t* vr = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh + (int64_t)min(key, p.Sk - 1) * p.v_ss;
+    // padded copies: key < Skp and d < DP always lie inside
+    const uint16_t* kr = p.k16 + ((int64_t)bk * p.Skp + key) * DP;
+    const uint16_t* vr = p.v16 + ((int64_t)bk * p.Skp + key) * DP;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int d = 16 * s + 8 * fk;
-      const bool ok = key < p.Sk && d < p.D;
-      kf[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(kr + d), sk) : make_uint4(0, 0, 0, 0));
-      *reinterpret_cast<uint4*>(sVw + swz_row<DP>(fr, 2 * s + fk)) =
-          ok ? cvt_bf16x8_f16x8(ldg16(vr + d), sv) : make_uint4(0, 0, 0, 0);
+      kf[s] = __builtin_bit_cast(half8, ldg16(kr + d));
+      *reinterpret_cast<uint4*>(sVw + swz_row<DP>(fr, 2 * s + fk)) = ldg16(vr + d);
     }
   }
   floatx16 dk[DB], dv[DB];
@@ -177,19 +224,17 @@ dkdv_kernel(BwdParams p) {
   const int total = group * (nqt - qt0);
 
   // tile staging: thread t moves 16-byte chunks t + 256 i (row c / CPR, chunk c % CPR)
-  // of the Q and dO tiles; rows past Sq and columns past D load as zeros
+  // of the Q16 and dO16 tiles (the padded copies: zeros past Sq and past D)
   uint4 rq[CH], rd[CH];
   auto gload = [&](int it) {
     const int h = hk * group + it / (nqt - qt0);
     const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
-    const uint16_t* qb = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
-    const uint16_t* db = p.dout + (int64_t)b * p.d_sb + (int64_t)h * p.d_sh;
+    const int64_t base = ((int64_t)(b * p.H + h) * p.Sqp + q0) * DP;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
-      const bool ok = q0 + row < p.Sq && ch * 8 < p.D;
-      rq[i] = ok ? ldg16(qb + (int64_t)(q0 + row) * p.q_ss + ch * 8) : make_uint4(0, 0, 0, 0);
-      rd[i] = ok ? ldg16(db + (int64_t)(q0 + row) * p.d_ss + ch * 8) : make_uint4(0, 0, 0, 0);
+      rq[i] = ldg16(p.q16 + base + row * DP + ch * 8);
+      rd[i] = ldg16(p.do16 + base + row * DP + ch * 8);
     }
   };
 
@@ -197,7 +242,6 @@ dkdv_kernel(BwdParams p) {
     const int h = hk * group + it / (nqt - qt0);
     const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
     const int bh = b * p.H + h;
-    const float sq = ldexp1(a), sdo = ldexp1(ev + G);
     // no register prefetch (it would cost the second block per CU): the loads are
     // issued before the barrier that waits for the previous tile's readers
     gload(it);
@@ -205,8 +249,8 @@ dkdv_kernel(BwdParams p) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
-      *reinterpret_cast<uint4*>(sQ + swz_row<DP>(row, ch)) = cvt_bf16x8_f16x8(rq[i], sq);
-      *reinterpret_cast<uint4*>(sD + swz_row<DP>(row, ch)) = cvt_bf16x8_f16x8(rd[i], sdo);
+      *reinterpret_cast<uint4*>(sQ + swz_row<DP>(row, ch)) = rq[i];
+      *reinterpret_cast<uint4*>(sD + swz_row<DP>(row, ch)) = rd[i];
     }
     if (tid < BQ) {
       const int qi = q0 + tid;
@@ -355,16 +399,14 @@ dq_kernel(BwdParams p) {
   half8 qf[KS];
   uint8_t* sDo = smem + 2 * TILE + wave * DOW;  // written and read by this wave only
   {
-    const float sq = ldexp1(a), sdo = ldexp1(ev + G);
-    const uint16_t* qr = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)min(qrow, p.Sq - 1) * p.q_ss;
-    const uint16_t* dr = p.dout + (int64_t)b * p.d_sb + (int64_t)h * p.d_sh + (int64_t)min(qrow, p.Sq - 1) * p.d_ss;
+    // padded copies: qrow < Sqp and d < DP always lie inside
+    const uint16_t* qr = p.q16 + ((int64_t)bh * p.Sqp + qrow) * DP;
+    const uint16_t* dr = p.do16 + ((int64_t)bh * p.Sqp + qrow) * DP;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int d = 16 * s + 8 * fk;
-      const bool ok = qrow < p.Sq && d < p.D;
-      qf[s] = __builtin_bit_cast(half8, ok ? cvt_bf16x8_f16x8(ldg16(qr + d), sq) : make_uint4(0, 0, 0, 0));
-      *reinterpret_cast<uint4*>(sDo + swz_row<DP>(fr, 2 * s + fk)) =
-          ok ? cvt_bf16x8_f16x8(ldg16(dr + d), sdo) : make_uint4(0, 0, 0, 0);
+      qf[s] = __builtin_bit_cast(half8, ldg16(qr + d));
+      *reinterpret_cast<uint4*>(sDo + swz_row<DP>(fr, 2 * s + fk)) = ldg16(dr + d);
     }
   }
   const float lse_q = qrow < p.Sq ? p.lse[(int64_t)bh * p.Sq + qrow] : INFINITY;
@@ -377,19 +419,17 @@ dq_kernel(BwdParams p) {
 
   const int nkb_all = (p.Sk + BKV - 1) / BKV;
   const int nkb = CAUSAL ? min(nkb_all, (min(q0 + BQ, p.Sq) + BKV - 1) / BKV) : nkb_all;
-  const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-  const uint16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
-  const float sk = ldexp1(-a), sv = ldexp1(-ev);
+  const uint16_t* kbase = p.k16 + (int64_t)(b * p.Hkv + hk) * p.Skp * DP;
+  const uint16_t* vbase = p.v16 + (int64_t)(b * p.Hkv + hk) * p.Skp * DP;
   // tile staging: thread t moves 16-byte chunks t + 256 i (row c / CPR, chunk
-  // c % CPR) of the K and V tiles; rows past Sk and columns past D load as zeros
+  // c % CPR) of the K16 and V16 tiles (the padded copies: zeros past Sk and D)
   uint4 rk[CH], rv[CH];
   auto gload = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * NTH, row = kb * BKV + c / CPR, ch = c % CPR;
-      const bool ok = row < p.Sk && ch * 8 < p.D;
-      rk[i] = ok ? ldg16(kbase + (int64_t)row * p.k_ss + ch * 8) : make_uint4(0, 0, 0, 0);
-      rv[i] = ok ? ldg16(vbase + (int64_t)row * p.v_ss + ch * 8) : make_uint4(0, 0, 0, 0);
+      rk[i] = ldg16(kbase + row * DP + ch * 8);
+      rv[i] = ldg16(vbase + row * DP + ch * 8);
     }
   };
   const uint16_t* brow = nullptr;
@@ -402,8 +442,8 @@ dq_kernel(BwdParams p) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
-      *reinterpret_cast<uint4*>(sK + swz_row<DP>(row, ch)) = cvt_bf16x8_f16x8(rk[i], sk);
-      *reinterpret_cast<uint4*>(sV + swz_row<DP>(row, ch)) = cvt_bf16x8_f16x8(rv[i], sv);
+      *reinterpret_cast<uint4*>(sK + swz_row<DP>(row, ch)) = rk[i];
+      *reinterpret_cast<uint4*>(sV + swz_row<DP>(row, ch)) = rv[i];
     }
     __syncthreads();
     if (kb + 1 < nkb) gload(kb + 1);
@@ -485,15 +525,25 @@ dq_kernel(BwdParams p) {
 }
 
 struct BwdWs {
-  int64_t nch;
-  size_t off_delta, total;
+  int64_t nch, Sqp, Skp, DP;
+  size_t off_delta, off_q16, off_do16, off_k16, off_v16, total;
 };
 
-BwdWs bwd_ws(int64_t B, int64_t H, int64_t Sq) {
+// partial dO maxima | delta (B, H, Sq) fp32 | q16, dO16 (B, H, Sqp, DP) | k16, v16
+// (B, Hkv, Skp, DP), rows padded to a multiple of 128, DP = 64 or 128
+BwdWs bwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
   BwdWs w;
   w.nch = head_amax_chunks(B * H, Sq);
+  w.Sqp = cdiv(Sq, 128) * 128;
+  w.Skp = cdiv(Sk, 128) * 128;
+  w.DP = D <= 64 ? 64 : 128;
   w.off_delta = align_up((size_t)(B * H * w.nch) * 4, 256);
-  w.total = w.off_delta + align_up((size_t)(B * H * Sq) * 4, 256);
+  w.off_q16 = w.off_delta + align_up((size_t)(B * H * Sq) * 4, 256);
+  const size_t qb = align_up((size_t)(B * H * w.Sqp * w.DP) * 2, 256), kb = align_up((size_t)(B * Hkv * w.Skp * w.DP) * 2, 256);
+  w.off_do16 = w.off_q16 + qb;
+  w.off_k16 = w.off_do16 + qb;
+  w.off_v16 = w.off_k16 + kb;
+  w.total = w.off_v16 + kb;
   return w;
 }
 
@@ -518,8 +568,7 @@ int launch_bwd_dp(const BwdParams& p, bool causal, bool has_bias, hipStream_t st
 }  // namespace
 
 extern "C" size_t tbf16_attn_bwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
-  (void)Hkv; (void)Sk; (void)D;
-  return bwd_ws(B, H, Sq).total;
+  return bwd_ws(B, H, Hkv, Sq, Sk, D).total;
 }
 
 extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const void* o16, const float* lse,
@@ -540,7 +589,7 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
                aligned16(dk) && aligned16(dv),
            "attn_bwd: tensors must be 16-byte aligned");
   if (bias) TB_CHECK(bias_strides != nullptr, "attn_bwd: bias strides missing");
-  const BwdWs w = bwd_ws(B, H, Sq);
+  const BwdWs w = bwd_ws(B, H, Hkv, Sq, Sk, D);
   TB_CHECK(ws != nullptr && ws_bytes >= (int64_t)w.total, "attn_bwd: workspace too small");
   if (B == 0 || Sq == 0 || Sk == 0) return 0;
   hipStream_t st = as_stream(stream);
@@ -563,7 +612,18 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
   p.delta = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_delta);
   p.exps_out = exps_out; p.overflow = overflow;
   p.dq = (uint16_t*)dq; p.dk = (uint16_t*)dk; p.dv = (uint16_t*)dv;
-  delta_kernel<<<dim3((unsigned)cdiv(Sq, 16), (unsigned)(B * H)), NTH, 0, st>>>(p);
+  char* wsb = reinterpret_cast<char*>(ws);
+  p.q16 = reinterpret_cast<uint16_t*>(wsb + w.off_q16);
+  p.do16 = reinterpret_cast<uint16_t*>(wsb + w.off_do16);
+  p.k16 = reinterpret_cast<uint16_t*>(wsb + w.off_k16);
+  p.v16 = reinterpret_cast<uint16_t*>(wsb + w.off_v16);
+  p.Sqp = (int)w.Sqp; p.Skp = (int)w.Skp; p.DPc = (int)w.DP;
+  {
+    const int64_t rpb = NTH / (w.DP / 8);
+    prep_kernel<<<dim3((unsigned)cdiv(std::max(w.Sqp, w.Skp), 4 * rpb), (unsigned)(B * H + 2 * B * Hkv)), NTH, 0, st>>>(p);
+    TB_LAUNCH_CHECK("attn_bwd/prep");
+  }
+  delta_kernel<<<dim3((unsigned)cdiv(w.Sqp, 16), (unsigned)(B * H)), NTH, 0, st>>>(p);
   TB_LAUNCH_CHECK("attn_bwd/delta");
   if (D <= 64) return launch_bwd_dp<64>(p, causal != 0, bias != nullptr, st);
   return launch_bwd_dp<128>(p, causal != 0, bias != nullptr, st);

@@ -160,13 +160,21 @@ __device__ __forceinline__ uint4 buf_load16(BufRes r, int voffset, int soffset) 
 // ---- LDS tiles ---------------------------------------------------------------
 
 // Byte offset of 16-byte chunk `chunk` of row `row` in a row-major DP-wide fp16 LDS
-// tile, the chunk index XOR-swizzled by row so that 16 lanes reading one chunk of
-// 16 consecutive rows (ds_read_b128 fragments) hit distinct banks: by row % 16
-// for 256-byte (or longer) rows, by (row / 2) % 8 for 128-byte rows.
+// tile, the chunk index XOR-swizzled by row. Two read patterns must be bank-
+// conflict free (a pass of a wave's LDS read covers 256 bytes = all 64 banks):
+//  (a) ds_read_b128 fragments: 16 lanes read one logical chunk of 16 consecutive
+//      rows (16-aligned);
+//  (b) ds_read_b64_tr_b16 fragments (tr_frag): 32 lanes read 4 consecutive chunks
+//      (4-aligned) of 4 consecutive rows (4-aligned).
+// 256-byte rows (every row starts at bank 0): chunk ^ g(row) with g the row's low
+// 4 bits with their 2-bit halves swapped, a bijection on 16 rows for (a), and
+// for (b) the 4 rows differ in g's top two bits, which move the 4-chunk group.
+// 128-byte rows (row parity picks the bank half): chunk ^ h(row) with h a
+// bijection on rows 2 apart for (a), whose top bit is row bit 1 for (b).
 template <int DP>
 __device__ __forceinline__ int swz_row(int row, int chunk) {
-  if constexpr (DP >= 128) return row * (DP * 2) + ((chunk ^ (row & 15)) << 4);
-  else return row * (DP * 2) + ((chunk ^ ((row >> 1) & 7)) << 4);
+  if constexpr (DP >= 128) return row * (DP * 2) + ((chunk ^ (((row & 3) << 2) | ((row >> 2) & 3))) << 4);
+  else return row * (DP * 2) + ((chunk ^ ((((row >> 1) & 1) << 2) | ((row >> 2) & 3))) << 4);
 }
 
 // Byte offset of the 8-byte run starting at column col (a multiple of 4).
