@@ -4,8 +4,12 @@
 // per-head partial maxima written by a memory-bound pre-pass:
 //   eq = max_{b,h} frexp(amax q[b,h]), ek likewise, a = floor((ek - eq) / 2)
 //   clamped to [ek - 14, 14 - eq], ev[b, hkv] = frexp(amax v[b, hkv]) - v_exp.
-// q, k, v are read as bf16 and converted on the fly: q16 = q * 2^a, k16 = k * 2^-a,
-// v16 = v * 2^-ev (exact powers of two), so no scaled copies exist in HBM.
+// A one-block pass finalises the exponents; a conversion pass then writes k16 =
+// k * 2^-a and v16 = v * 2^-ev (exact powers of two) to the workspace as fp16, k16
+// row-major (B, Hkv, Skp, DP) and v16 transposed (B, Hkv, DP, Skp) with keys
+// permuted as the PV operand wants them, both zero-padded, so the forward kernel
+// stages K and V tiles as plain copies: each K/V element is converted once instead
+// of once per query block. q16 = q * 2^a is converted on the fly (once per row).
 //
 // Block = 4 or 8 waves, 32 query rows per wave; key tiles of 64.
 //  - a wave keeps its 32 q rows as MFMA fragments in registers for the whole
@@ -46,6 +50,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 struct FwdParams {
   const uint16_t *q, *k, *v;
+  uint16_t *k16, *vt16;  // workspace copies: (B, Hkv, Skp, DP) and (B, Hkv, DP, Skp)
+  int32_t* ex;           // workspace exponents {a, 0, ev[b * Hkv + hk]...}
+  int Skp, DPc;
   int64_t q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss;
   const uint16_t* bias;
   int64_t bias_sb, bias_sh, bias_sq;
@@ -126,6 +133,79 @@ __device__ __forceinline__ uint2 gather4(uint32_t w0, uint32_t w1, uint32_t w2, 
   return make_uint2(__builtin_amdgcn_perm(w1, w0, sel), __builtin_amdgcn_perm(w3, w2, sel));
 }
 
+// Exponents (tbf16/attention.py:267-277) from the per-head partial maxima, once:
+// a and ev[b * Hkv + hk] into the workspace (and into the caller's exps if given).
+__global__ __launch_bounds__(256) void attn_exps_kernel(FwdParams p) {
+  __shared__ int red[4];
+  const int eq = heads_max_exp<256>(p.part_q, p.B * p.H, p.nch_q, red);
+  const int ek = heads_max_exp<256>(p.part_k, p.B * p.Hkv, p.nch_k, red);
+  int a = (ek - eq) >> 1;  // floor division
+  a = max(min(a, 14 - eq), ek - 14);
+  if (threadIdx.x == 0) {
+    p.ex[0] = a;
+    p.ex[1] = 0;
+    if (p.exps) {
+      p.exps[0] = a;
+      p.exps[1] = 0;
+    }
+  }
+  for (int i = threadIdx.x; i < p.B * p.Hkv; i += 256) {
+    const int ev = head_exp_of(p.part_v, i, p.nch_v) - p.v_exp;
+    p.ex[2 + i] = ev;
+    if (p.exps) p.exps[2 + i] = ev;
+  }
+}
+
+// k16 and the permuted v16^T for one 64-key tile of one (batch, kv head): block
+// (tile, b * Hkv + hk), 256 threads. K: thread t converts 16-byte chunks t + 256 i
+// (row c / (DP / 8), chunk c % (DP / 8)). V: thread t takes blocks t + 256 i of 4
+// keys x 8 columns (kg = block % 16, dc = block / 16), converts the four 16-byte
+// row pieces and writes, for each of its 8 columns d, the 4-key run at position
+// perm16(4 kg) of row d (8 bytes; the 16 threads of one dc fill each row segment).
+// Keys past Sk and columns past D are written as zeros.
+template <int DP>
+__global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
+  constexpr int CPR = DP / 8;
+  const int bhk = blockIdx.y, b = bhk / p.Hkv, hk = bhk % p.Hkv;
+  const int key0 = blockIdx.x * BKV;
+  const int a = p.ex[0], ev = p.ex[2 + bhk];
+  const float sk = ldexp1(-a), sv = ldexp1(-ev);
+  const uint16_t* kb = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const uint16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
+  uint16_t* k16 = p.k16 + ((int64_t)bhk * p.Skp + key0) * DP;
+  uint16_t* vt16 = p.vt16 + (int64_t)bhk * DP * p.Skp + key0;
+#pragma unroll
+  for (int i = 0; i < BKV * CPR / 256; ++i) {
+    const int c = threadIdx.x + i * 256, row = c / CPR, ch = c % CPR;
+    const int key = key0 + row;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (key < p.Sk && ch * 8 < p.D) v = cvt_bf16x8_f16x8(ldg16(kb + (int64_t)key * p.k_ss + ch * 8), sk);
+    stg16(k16 + row * DP + ch * 8, v);
+  }
+#pragma unroll
+  for (int i = 0; i < (16 * CPR + 255) / 256; ++i) {
+    const int blk = threadIdx.x + i * 256;
+    if (blk >= 16 * CPR) break;
+    const int kg = blk & 15, dc = blk >> 4;
+    uint4 cv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = key0 + 4 * kg + r;
+      cv[r] = make_uint4(0, 0, 0, 0);
+      if (key < p.Sk && dc * 8 < p.D) cv[r] = cvt_bf16x8_f16x8(ldg16(vb + (int64_t)key * p.v_ss + dc * 8), sv);
+    }
+    const int pos = perm16(4 * kg);
+    const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
+    const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
+    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&cv[2]);
+    const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<uint2*>(vt16 + (int64_t)(dc * 8 + j) * p.Skp + pos) =
+          gather4(w0[j >> 1], w1[j >> 1], w2[j >> 1], w3[j >> 1], j & 1);
+  }
+}
+
 // Forward kernel: NW waves, 32 query rows each (BQ = 32 * NW), 64-key tiles.
 // NW = 8 (two waves per SIMD, K/V conversion shared by 256 queries): waves 0-3
 // stage K, waves 4-7 stage V^T. NW = 4: every thread stages both. PF register
@@ -141,12 +221,11 @@ attn_fwd_kernel(FwdParams p) {
   constexpr int VTH = NW == 8 ? NT / 2 : NT;  // threads staging V
   constexpr int VT0 = NW == 8 ? NT / 2 : 0;   // first V-staging thread
   constexpr int KL = BKV * CPR / KTH;         // K chunks per staging thread
-  constexpr int VBLK = 16 * CPR;              // 4-key x 8-d blocks in a V tile
-  constexpr int VL = (VBLK + VTH - 1) / VTH;  // V blocks per staging thread
-  static_assert(KL * KTH == BKV * CPR, "K staging");
-  // one staging array shared by the K and V roles: [K chunks][V blocks x 4 rows]
+  constexpr int VL = DP * 8 / VTH;            // V^T chunks (8 per row of 64 keys)
+  static_assert(KL * KTH == BKV * CPR && VL * VTH == DP * 8, "K/V staging");
+  // one staging array shared by the K and V roles: [K chunks][V^T chunks]
   constexpr int VOFF = NW == 8 ? 0 : KL;
-  constexpr int SL = NW == 8 ? (KL > 4 * VL ? KL : 4 * VL) : KL + 4 * VL;
+  constexpr int SL = NW == 8 ? (KL > VL ? KL : VL) : KL + VL;
   constexpr int KBYTES = BKV * DP * 2;
   constexpr int STAGE = KBYTES + DP * 128;
   __shared__ __align__(16) uint8_t smem[2 * STAGE];
@@ -157,20 +236,10 @@ attn_fwd_kernel(FwdParams p) {
   const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
   const int hk = h / (p.H / p.Hkv);
 
-  // ---- exponents ----
-  const int eq = heads_max_exp<NT>(p.part_q, p.B * p.H, p.nch_q, red);
-  const int ek = heads_max_exp<NT>(p.part_k, p.B * p.Hkv, p.nch_k, red);
-  int a = (ek - eq) >> 1;  // floor division
-  a = max(min(a, 14 - eq), ek - 14);
-  const int ev = head_exp_of(p.part_v, b * p.Hkv + hk, p.nch_v) - p.v_exp;
-  if (p.exps && blockIdx.x == 0 && blockIdx.y == 0) {
-    if (tid == 0) {
-      p.exps[0] = a;
-      p.exps[1] = 0;
-    }
-    for (int i = tid; i < p.B * p.Hkv; i += NT) p.exps[2 + i] = head_exp_of(p.part_v, i, p.nch_v) - p.v_exp;
-  }
-  const float sq = ldexp1(a), sk = ldexp1(-a), sv = ldexp1(-ev);
+  // ---- exponents (finalised by attn_exps_kernel) ----
+  const int a = p.ex[0];
+  const int ev = p.ex[2 + b * p.Hkv + hk];
+  const float sq = ldexp1(a);
 
   // Query tiles of this block: one, or with pair (causal) the heavy tile
   // ntiles-1-x and then the light tile x, so every block does the same work.
@@ -194,34 +263,27 @@ attn_fwd_kernel(FwdParams p) {
       }
     }
 
-    // ---- K / V staging through buffer loads (rows past Sk load as zeros) ----
-    const BufRes kres = make_res(p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh,
-                                 min<int64_t>((int64_t)p.Sk * p.k_ss * 2, 0x7fffffff));
-    const BufRes vres = make_res(p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh,
-                                 min<int64_t>((int64_t)p.Sk * p.v_ss * 2, 0x7fffffff));
+    // ---- K / V^T staging: plain 16-byte copies of the workspace's converted tiles ----
+    const int bhk = b * p.Hkv + hk;
+    const BufRes kres = make_res(p.k16 + (int64_t)bhk * p.Skp * DP, min<int64_t>((int64_t)p.Skp * DP * 2, 0x7fffffff));
+    const BufRes vres = make_res(p.vt16 + (int64_t)bhk * DP * p.Skp, min<int64_t>((int64_t)DP * p.Skp * 2, 0x7fffffff));
     const bool k_stager = NW != 8 || tid < KTH;
     const bool v_stager = NW != 8 || tid >= VT0;
-    const int ktid = NW == 8 ? tid : tid, vtid = tid - VT0;
+    const int ktid = tid, vtid = tid - VT0;
     uint4 st[PF][SL];
     auto gload = [&](uint4(&sr)[SL], int kb) {
-      const int soff_k = kb * BKV * (int)p.k_ss * 2, soff_v = kb * BKV * (int)p.v_ss * 2;
       if (k_stager) {
   #pragma unroll
         for (int i = 0; i < KL; ++i) {
           const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
-          sr[i] = buf_load16(kres, (row * (int)p.k_ss + ch * 8) * 2, soff_k);
+          sr[i] = buf_load16(kres, (row * DP + ch * 8) * 2, kb * BKV * DP * 2);
         }
       }
       if (v_stager) {
   #pragma unroll
         for (int i = 0; i < VL; ++i) {
-          const int blk = vtid + i * VTH;
-          const int kg = blk & 15, dc = blk >> 4;
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            // d >= D rows of V^T only feed O^T rows that are never written: no zeroing
-            sr[VOFF + 4 * i + r] = buf_load16(vres, ((4 * kg + r) * (int)p.v_ss + dc * 8) * 2, soff_v);
-          }
+          const int c = vtid + i * VTH, d = c >> 3, ch = c & 7;
+          sr[VOFF + i] = buf_load16(vres, (d * p.Skp + ch * 8) * 2, kb * BKV * 2);
         }
       }
     };
@@ -229,37 +291,17 @@ attn_fwd_kernel(FwdParams p) {
       uint8_t* sK = smem + stg * STAGE;
       uint8_t* sV = sK + KBYTES;
       if (k_stager) {
-        // K columns d >= D (the next row's values when D < DP) meet zero Q columns,
-        // but must be zero themselves so that no inf or nan there reaches S
-        const bool kpad = p.D < DP;
   #pragma unroll
         for (int i = 0; i < KL; ++i) {
           const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
-          uint4 v = sr[i];
-          if (kpad) v = ch * 8 < p.D ? v : make_uint4(0, 0, 0, 0);
-          *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, ch)) = cvt_bf16x8_f16x8(v, sk);
+          *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, ch)) = sr[i];
         }
       }
       if (v_stager) {
   #pragma unroll
         for (int i = 0; i < VL; ++i) {
-          const int blk = vtid + i * VTH;
-          if (blk >= VBLK) continue;
-          const int kg = blk & 15, dc = blk >> 4;
-          uint4 cv[4];
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) cv[r] = cvt_bf16x8_f16x8(sr[VOFF + 4 * i + r], sv);
-          const int pos = perm16(4 * kg);  // 4 consecutive keys stay consecutive
-          const int chunk = pos >> 3, half_off = (pos & 7) * 2;
-          const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
-          const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
-          const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&cv[2]);
-          const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
-  #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const uint2 g = gather4(w0[j >> 1], w1[j >> 1], w2[j >> 1], w3[j >> 1], j & 1);
-            *reinterpret_cast<uint2*>(sV + swz_vt(dc * 8 + j, chunk) + half_off) = g;
-          }
+          const int c = vtid + i * VTH, d = c >> 3, ch = c & 7;
+          *reinterpret_cast<uint4*>(sV + swz_vt(d, ch)) = sr[VOFF + i];
         }
       }
     };
@@ -412,19 +454,27 @@ attn_fwd_kernel(FwdParams p) {
 }
 
 struct WsLayout {
-  int64_t nch_q, nch_k, nch_v;
-  size_t off_k, off_v, total;
+  int64_t nch_q, nch_k, nch_v, Skp, DP;
+  size_t off_k, off_v, off_ex, off_k16, off_vt16, total;
 };
 
-WsLayout fwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk) {
+// partial maxima of q | k | v, exponents {a, 0, ev...}, k16 (B, Hkv, Skp, DP),
+// v16^T (B, Hkv, DP, Skp); Skp = Sk rounded up to the 64-key tile
+WsLayout fwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
   WsLayout w;
   w.nch_q = head_amax_chunks(B * H, Sq);
   w.nch_k = head_amax_chunks(B * Hkv, Sk);
   w.nch_v = w.nch_k;
+  w.Skp = cdiv(Sk, BKV) * BKV;
+  w.DP = D <= 64 ? 64 : D <= 128 ? 128 : 256;
   const size_t bq = align_up((size_t)(B * H * w.nch_q) * 4, 256), bk = align_up((size_t)(B * Hkv * w.nch_k) * 4, 256);
+  const size_t bkv = align_up((size_t)(B * Hkv * w.Skp * w.DP) * 2, 256);
   w.off_k = bq;
   w.off_v = bq + bk;
-  w.total = bq + 2 * bk;
+  w.off_ex = bq + 2 * bk;
+  w.off_k16 = w.off_ex + align_up((size_t)(2 + B * Hkv) * 4, 256);
+  w.off_vt16 = w.off_k16 + bkv;
+  w.total = w.off_vt16 + bkv;
   return w;
 }
 
@@ -478,8 +528,7 @@ int check_bhsd(const char* fn, const char* name, const void* x, const int64_t* s
 }  // namespace
 
 extern "C" size_t tbf16_attn_fwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
-  (void)D;
-  return fwd_ws(B, H, Hkv, Sq, Sk).total;
+  return fwd_ws(B, H, Hkv, Sq, Sk, D).total;
 }
 
 extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t Hkv,
@@ -496,7 +545,7 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   if (int rc = check_bhsd("attn_fwd", "v", v, v_strides, D)) return rc;
   TB_CHECK(o != nullptr && aligned16(o) && (o16 == nullptr || aligned16(o16)), "attn_fwd: bad output");
   if (bias) TB_CHECK(bias_strides != nullptr, "attn_fwd: bias strides missing");
-  const WsLayout w = fwd_ws(B, H, Hkv, Sq, Sk);
+  const WsLayout w = fwd_ws(B, H, Hkv, Sq, Sk, D);
   TB_CHECK(ws != nullptr && ws_bytes >= (int64_t)w.total, "attn_fwd: workspace too small");
   if (B == 0 || Sq == 0) return 0;
   TB_CHECK(Sk > 0, "attn_fwd: empty key sequence");
@@ -534,6 +583,21 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   p.o16 = (uint16_t*)o16;
   p.exps = exps;
   p.pair = 0;
+  char* wsb = reinterpret_cast<char*>(ws);
+  p.ex = reinterpret_cast<int32_t*>(wsb + w.off_ex);
+  p.k16 = reinterpret_cast<uint16_t*>(wsb + w.off_k16);
+  p.vt16 = reinterpret_cast<uint16_t*>(wsb + w.off_vt16);
+  p.Skp = (int)w.Skp;
+  p.DPc = (int)w.DP;
+  attn_exps_kernel<<<1, 256, 0, st>>>(p);
+  TB_LAUNCH_CHECK("attn_fwd/exps");
+  {
+    const dim3 g((unsigned)(w.Skp / BKV), (unsigned)(B * Hkv));
+    if (w.DP == 64) kv_prep_kernel<64><<<g, 256, 0, st>>>(p);
+    else if (w.DP == 128) kv_prep_kernel<128><<<g, 256, 0, st>>>(p);
+    else kv_prep_kernel<256><<<g, 256, 0, st>>>(p);
+    TB_LAUNCH_CHECK("attn_fwd/kv_prep");
+  }
   const char* ov = getenv("TBF16_ATTN_WAVES");  // benchmarking override: 4 or 8
   const int nw = ov ? atoi(ov) : 0;
   if (D <= 64) return launch_fwd_dp<64>(p, causal != 0, bias != nullptr, st, nw);
