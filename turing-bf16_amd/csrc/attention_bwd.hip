@@ -177,17 +177,16 @@ __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
 template <int DP, bool CAUSAL, bool HAS_BIAS>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS ? 1 : 2, HAS_BIAS ? 1 : 2))) void
 dkdv_kernel(BwdParams p) {
-  constexpr int BQ = 64, BK = 128;
+  constexpr int BQ = 32, BK = 128;
   constexpr int KS = DP / 16, DB = DP / 32, CPR = DP / 8;
-  constexpr int TILE = BQ * DP * 2;   // one 64 x DP fp16 tile
+  constexpr int TILE = BQ * DP * 2;   // one 32 x DP fp16 tile
   constexpr int VW = 32 * DP * 2;     // one wave's V rows
   constexpr int CH = BQ * CPR / NTH;  // 16-byte chunks per thread per tile
-  constexpr int MAIN = 4 * VW + 2 * TILE, OUT = BK * DP * 4;
+  constexpr int STG = 2 * TILE;       // one stage: Q16 and dO16 tiles
+  constexpr int MAIN = 4 * VW + 2 * STG, OUT = BK * DP * 4;
   __shared__ __align__(16) uint8_t smem[MAIN > OUT ? MAIN : OUT];
-  __shared__ __align__(16) float s_lse[BQ];
-  __shared__ __align__(16) float s_delta[BQ];
-  uint8_t* sQ = smem + 4 * VW;
-  uint8_t* sD = sQ + TILE;
+  __shared__ __align__(16) float s_lse[2][BQ];
+  __shared__ __align__(16) float s_delta[2][BQ];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, fr = lane & 31, fk = lane >> 5;
   const int bk = blockIdx.y, b = bk / p.Hkv, hk = bk % p.Hkv;
@@ -223,29 +222,34 @@ dkdv_kernel(BwdParams p) {
   const int qt0 = CAUSAL ? min(k0 / BQ, nqt) : 0;
   const int total = group * (nqt - qt0);
 
-  // tile staging: thread t moves 16-byte chunks t + 256 i (row c / CPR, chunk c % CPR)
-  // of the Q16 and dO16 tiles (the padded copies: zeros past Sq and past D)
+  // Query tiles of 32 rows in two LDS stages (tile it in stage it % 2). The loads
+  // of tile it + 1 (thread t: 16-byte chunks t + 256 i of the Q16 and dO16 tiles,
+  // threads < 32 also the rows' lse and delta) are issued when tile it starts
+  // and stored into the other stage after tile it's S / dP products, so they
+  // have those MFMAs to land; one barrier per tile publishes the stage and
+  // retires the reads of the one it overwrote.
   uint4 rq[CH], rd[CH];
+  float rl = INFINITY, rdl = 0.f;
   auto gload = [&](int it) {
     const int h = hk * group + it / (nqt - qt0);
     const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
-    const int64_t base = ((int64_t)(b * p.H + h) * p.Sqp + q0) * DP;
+    const int bh = b * p.H + h;
+    const int64_t base = ((int64_t)bh * p.Sqp + q0) * DP;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
       rq[i] = ldg16(p.q16 + base + row * DP + ch * 8);
       rd[i] = ldg16(p.do16 + base + row * DP + ch * 8);
     }
+    if (tid < BQ) {
+      const int qi = q0 + tid;
+      rl = qi < p.Sq ? p.lse[(int64_t)bh * p.Sq + qi] : INFINITY;
+      rdl = qi < p.Sq ? p.delta[(int64_t)bh * p.Sq + qi] : 0.f;
+    }
   };
-
-  for (int it = 0; it < total; ++it) {
-    const int h = hk * group + it / (nqt - qt0);
-    const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
-    const int bh = b * p.H + h;
-    // no register prefetch (it would cost the second block per CU): the loads are
-    // issued before the barrier that waits for the previous tile's readers
-    gload(it);
-    __syncthreads();
+  auto lstore = [&](int stg) {
+    uint8_t* sQ = smem + 4 * VW + stg * STG;
+    uint8_t* sD = sQ + TILE;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
@@ -253,84 +257,97 @@ dkdv_kernel(BwdParams p) {
       *reinterpret_cast<uint4*>(sD + swz_row<DP>(row, ch)) = rd[i];
     }
     if (tid < BQ) {
-      const int qi = q0 + tid;
-      s_lse[tid] = qi < p.Sq ? p.lse[(int64_t)bh * p.Sq + qi] : INFINITY;
-      s_delta[tid] = qi < p.Sq ? p.delta[(int64_t)bh * p.Sq + qi] : 0.f;
+      s_lse[stg][tid] = rl;
+      s_delta[stg][tid] = rdl;
     }
-    __syncthreads();
+  };
+
+  if (total > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int it = 0; it < total; ++it) {
+    const int stg = it & 1;
+    const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
+    const uint8_t* sQ = smem + 4 * VW + stg * STG;
+    const uint8_t* sD = sQ + TILE;
+    const bool more = it + 1 < total;
+    if (more) gload(it + 1);
 
     const bool edge = q0 + BQ > p.Sq || k0 + BK > p.Sk || (CAUSAL && k0 + wave * 32 + 31 >= q0);
     // with a bias the logits are scaled and biased first, as in the forward pass
     const float cs = HAS_BIAS ? 1.f : p.scale_log2;
+    const int h = hk * group + it / (nqt - qt0);
+    // S and dP for the tile's 32 queries: lane = one key, 16 queries
+    floatx16 sacc, pacc;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      // S and dP for 32 queries: lane = one key, 16 queries
-      floatx16 sacc, pacc;
+    for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+    for (int s = 0; s < KS; ++s) {
+      const half8 qa = *reinterpret_cast<const half8*>(sQ + swz_row<DP>(fr, 2 * s + fk));
+      const half8 da = *reinterpret_cast<const half8*>(sD + swz_row<DP>(fr, 2 * s + fk));
+      const half8 vb = *reinterpret_cast<const half8*>(sVw + swz_row<DP>(fr, 2 * s + fk));
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kf[s], sacc, 0, 0, 0);
+      pacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, vb, pacc, 0, 0, 0);
+    }
+    // the next tile's stage: its reads retired at the previous barrier
+    if (more) lstore(stg ^ 1);
+    if constexpr (HAS_BIAS) {
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const half8 qa = *reinterpret_cast<const half8*>(sQ + swz_row<DP>(qb * 32 + fr, 2 * s + fk));
-        const half8 da = *reinterpret_cast<const half8*>(sD + swz_row<DP>(qb * 32 + fr, 2 * s + fk));
-        const half8 vb = *reinterpret_cast<const half8*>(sVw + swz_row<DP>(fr, 2 * s + fk));
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kf[s], sacc, 0, 0, 0);
-        pacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, vb, pacc, 0, 0, 0);
-      }
-      if constexpr (HAS_BIAS) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qi = q0 + qb * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-          if (qi < p.Sq && key < p.Sk)
-            sacc[r] = sacc[r] * p.scale_log2 +
-                      (float)__builtin_bit_cast(_Float16, p.bias[(int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh +
-                                                                 (int64_t)qi * p.bias_sq + key]) * kLog2e;
-          else
-            sacc[r] *= p.scale_log2;
-        }
-      }
-      // masking only where the tile crosses the diagonal or an end
-      if (edge) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qi = q0 + qb * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-          if (key >= p.Sk || qi >= p.Sq || (CAUSAL && key > qi)) sacc[r] = -INFINITY;
-        }
-      }
-      // P and dS (fp16, packed in MFMA k-slot order); the lane's 16 queries are 4
-      // runs of 4 (q = 32 qb + 8 i + 4 fk + j), so lse and delta come as float4s
-      uint32_t pp[8], ds[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ql0 = qb * 32 + 8 * i + 4 * fk;
-        const float4 l4 = *reinterpret_cast<const float4*>(s_lse + ql0);
-        const float4 d4 = *reinterpret_cast<const float4*>(s_delta + ql0);
-        const float lse4[4] = {l4.x, l4.y, l4.z, l4.w}, del4[4] = {d4.x, d4.y, d4.z, d4.w};
-        float pv[4], dsv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[4 * i + j], cs, -lse4[j]));
-          dsv[j] = pv[j] * (pacc[4 * i + j] - del4[j]);
-        }
-        pp[2 * i] = pack_f16(pv[0], pv[1]);
-        pp[2 * i + 1] = pack_f16(pv[2], pv[3]);
-        ds[2 * i] = pack_f16(dsv[0], dsv[1]);
-        ds[2 * i + 1] = pack_f16(dsv[2], dsv[3]);
-      }
-      // dV += P^T dO16, dK += dS^T Q16 over the half's two 16-query steps
-#pragma unroll
-      for (int kq = 0; kq < 2; ++kq) {
-        const int o = 4 * kq, r0 = qb * 32 + 16 * kq;
-        const half8 pa = __builtin_bit_cast(half8, make_uint4(pp[o], pp[o + 1], pp[o + 2], pp[o + 3]));
-        const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[o], ds[o + 1], ds[o + 2], ds[o + 3]));
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const half8 dob = tr_frag<DP>(sD, r0, db * 32, lane);
-          const half8 qbf = tr_frag<DP>(sQ, r0, db * 32, lane);
-          dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, dob, dv[db], 0, 0, 0);
-          dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, qbf, dk[db], 0, 0, 0);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int qi = q0 + 8 * (r >> 2) + 4 * fk + (r & 3);
+        if (qi < p.Sq && key < p.Sk)
+          sacc[r] = sacc[r] * p.scale_log2 +
+                    (float)__builtin_bit_cast(_Float16, p.bias[(int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh +
+                                                               (int64_t)qi * p.bias_sq + key]) * kLog2e;
+        else
+          sacc[r] *= p.scale_log2;
       }
     }
+    // masking only where the tile crosses the diagonal or an end
+    if (edge) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qi = q0 + 8 * (r >> 2) + 4 * fk + (r & 3);
+        if (key >= p.Sk || qi >= p.Sq || (CAUSAL && key > qi)) sacc[r] = -INFINITY;
+      }
+    }
+    // P and dS (fp16, packed in MFMA k-slot order); the lane's 16 queries are 4
+    // runs of 4 (q = 8 i + 4 fk + j), so lse and delta come as float4s
+    uint32_t pp[8], ds[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ql0 = 8 * i + 4 * fk;
+      const float4 l4 = *reinterpret_cast<const float4*>(&s_lse[stg][ql0]);
+      const float4 d4 = *reinterpret_cast<const float4*>(&s_delta[stg][ql0]);
+      const float lse4[4] = {l4.x, l4.y, l4.z, l4.w}, del4[4] = {d4.x, d4.y, d4.z, d4.w};
+      float pv[4], dsv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[4 * i + j], cs, -lse4[j]));
+        dsv[j] = pv[j] * (pacc[4 * i + j] - del4[j]);
+      }
+      pp[2 * i] = pack_f16(pv[0], pv[1]);
+      pp[2 * i + 1] = pack_f16(pv[2], pv[3]);
+      ds[2 * i] = pack_f16(dsv[0], dsv[1]);
+      ds[2 * i + 1] = pack_f16(dsv[2], dsv[3]);
+    }
+    // dV += P^T dO16, dK += dS^T Q16 over the tile's two 16-query steps
+#pragma unroll
+    for (int kq = 0; kq < 2; ++kq) {
+      const int o = 4 * kq, r0 = 16 * kq;
+      const half8 pa = __builtin_bit_cast(half8, make_uint4(pp[o], pp[o + 1], pp[o + 2], pp[o + 3]));
+      const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[o], ds[o + 1], ds[o + 2], ds[o + 3]));
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const half8 dob = tr_frag<DP>(sD, r0, db * 32, lane);
+        const half8 qbf = tr_frag<DP>(sQ, r0, db * 32, lane);
+        dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, dob, dv[db], 0, 0, 0);
+        dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, qbf, dk[db], 0, 0, 0);
+      }
+    }
+    __syncthreads();
   }
 
   // ---- epilogue: lane = key row (fr), d = db*32 + 8*(r/4) + 4*fk + r%4 ----
