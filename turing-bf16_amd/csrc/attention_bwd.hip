@@ -347,6 +347,15 @@ dkdv_kernel(BwdParams p) {
         dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, qbf, dk[db], 0, 0, 0);
       }
     }
+    // transposed reads one (kq, db) step ahead of their MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int s = 0; s + 1 < 2 * DB; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
   }
 
@@ -481,6 +490,15 @@ dq_kernel(BwdParams p) {
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[s], sacc, 0, 0, 0);
         pacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, dfs, pacc, 0, 0, 0);
       }
+      // fragment reads one k step ahead of the MFMAs that use them
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+      for (int s = 0; s + 1 < KS; ++s) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_barrier(0);
       const int kb0 = kb * BKV + kh * 32;
       if constexpr (HAS_BIAS) {
 #pragma unroll
@@ -514,6 +532,15 @@ dq_kernel(BwdParams p) {
           dq[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbf, sa, dq[db], 0, 0, 0);
         }
       }
+      // transposed reads one d block ahead of their MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int s = 0; s + 1 < 2 * DB; ++s) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
