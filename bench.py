@@ -168,6 +168,8 @@ def bench_train(iters: int):
     xg, wg = x.clone().requires_grad_(), w.clone().requires_grad_()
 
     def lin():
+        # a training step sees a new activation every time: no quantized-x cache hits
+        ag._x_cache.entries.clear()
         xg.grad = wg.grad = None
         ag.linear(xg, wg).backward(dy)
 

@@ -18,6 +18,19 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// One (B, H, S, D) bf16 tensor of a multi-tensor head-amax launch: BH = B * H heads,
+// strides sb / sh / ss, nch chunks of rows rows each, maxima into partial[bh * nch + c].
+struct AmaxSeg {
+  const uint16_t* x;
+  int64_t BH, H, S, sb, sh, ss, rows, nch;
+  float* partial;
+};
+struct AmaxSegs {
+  AmaxSeg seg[3];
+  int n;
+};
+int launch_head_amax3(const AmaxSegs& segs, int64_t D, hipStream_t st);
+
 }  // namespace tbf16
 
 #define TB_CHECK(cond, ...)           \

@@ -4,12 +4,13 @@
 // per-head partial maxima written by a memory-bound pre-pass:
 //   eq = max_{b,h} frexp(amax q[b,h]), ek likewise, a = floor((ek - eq) / 2)
 //   clamped to [ek - 14, 14 - eq], ev[b, hkv] = frexp(amax v[b, hkv]) - v_exp.
-// A one-block pass finalises the exponents; a conversion pass then writes k16 =
-// k * 2^-a and v16 = v * 2^-ev (exact powers of two) to the workspace as fp16, k16
-// row-major (B, Hkv, Skp, DP) and v16 transposed (B, Hkv, DP, Skp) with keys
-// permuted as the PV operand wants them, both zero-padded, so the forward kernel
-// stages K and V tiles as plain copies: each K/V element is converted once instead
-// of once per query block. q16 = q * 2^a is converted on the fly (once per row).
+// A conversion pass (whose blocks also derive a and ev from those maxima) writes
+// k16 = k * 2^-a and v16 = v * 2^-ev (exact powers of two) to the workspace as
+// fp16, k16 row-major (B, Hkv, Skp, DP) and v16 transposed (B, Hkv, DP, Skp) with
+// keys permuted as the PV operand wants them, both zero-padded, so the forward
+// kernel stages K and V tiles as plain copies: each K/V element is converted once
+// instead of once per query block. q16 = q * 2^a is converted on the fly (once per
+// row).
 //
 // Block = 4 or 8 waves, 32 query rows per wave; key tiles of 64.
 //  - a wave keeps its 32 q rows as MFMA fragments in registers for the whole
@@ -39,8 +40,6 @@ using namespace tbf16;
 
 namespace tbf16 {
 int64_t head_amax_chunks(int64_t BH, int64_t S);
-int launch_head_amax_partial(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
-                             int64_t sh, int64_t ss, float* partial, int64_t nchunks, hipStream_t st);
 }  // namespace tbf16
 
 namespace {
@@ -95,24 +94,6 @@ __device__ __forceinline__ int block_max_int(int v, int* red) {
   return r;
 }
 
-// max over heads of frexp(max over chunks of partial[bh][c])
-template <int NT>
-__device__ int heads_max_exp(const float* part, int nbh, int nch, int* red) {
-  int e = INT_MIN;
-  for (int bh = threadIdx.x; bh < nbh; bh += NT) {
-    float m = 0.f;
-    for (int c = 0; c < nch; ++c) m = fmaxf(m, part[bh * nch + c]);
-    e = max(e, frexp_exp(m));
-  }
-  return block_max_int<NT>(e, red);
-}
-
-__device__ __forceinline__ int head_exp_of(const float* part, int bh, int nch) {
-  float m = 0.f;
-  for (int c = 0; c < nch; ++c) m = fmaxf(m, part[bh * nch + c]);
-  return frexp_exp(m);
-}
-
 // Masks the scores of a key tile that crosses the end of the keys or (causal)
 // the diagonal: keys >= Sk or > qmax become -inf. Lane layout of S^T: key
 // key0 + 32 kh + 8 (r / 4) + 4 fk + r % 4 in accumulator r of half kh. Called
@@ -135,24 +116,29 @@ __device__ __forceinline__ uint2 gather4(uint32_t w0, uint32_t w1, uint32_t w2, 
 
 // Exponents (tbf16/attention.py:267-277) from the per-head partial maxima, once:
 // a and ev[b * Hkv + hk] into the workspace (and into the caller's exps if given).
-__global__ __launch_bounds__(256) void attn_exps_kernel(FwdParams p) {
-  __shared__ int red[4];
-  const int eq = heads_max_exp<256>(p.part_q, p.B * p.H, p.nch_q, red);
-  const int ek = heads_max_exp<256>(p.part_k, p.B * p.Hkv, p.nch_k, red);
-  int a = (ek - eq) >> 1;  // floor division
-  a = max(min(a, 14 - eq), ek - 14);
-  if (threadIdx.x == 0) {
-    p.ex[0] = a;
-    p.ex[1] = 0;
-    if (p.exps) {
-      p.exps[0] = a;
-      p.exps[1] = 0;
+// Per-head maxima of the partials, wave-parallel: wave w reduces heads w, w + 4,
+// ... (a lane per chunk), eight heads' loads in flight before any is reduced.
+// Calls f(head, max) on lane 0 of the reducing wave.
+template <typename F>
+__device__ __forceinline__ void heads_max(const float* part, int nbh, int nch, F f) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int bh0 = wave; bh0 < nbh; bh0 += 32) {
+    float m[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m[j] = 0.f;
+    for (int c = lane; c < nch; c += 64) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int bh = bh0 + 4 * j;
+        if (bh < nbh) m[j] = fmaxf(m[j], part[bh * nch + c]);
+      }
     }
-  }
-  for (int i = threadIdx.x; i < p.B * p.Hkv; i += 256) {
-    const int ev = head_exp_of(p.part_v, i, p.nch_v) - p.v_exp;
-    p.ex[2 + i] = ev;
-    if (p.exps) p.exps[2 + i] = ev;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int bh = bh0 + 4 * j;
+      const float mx = wave_max(m[j]);
+      if (bh < nbh && lane == 0) f(bh, mx);
+    }
   }
 }
 
@@ -163,12 +149,42 @@ __global__ __launch_bounds__(256) void attn_exps_kernel(FwdParams p) {
 // row pieces and writes, for each of its 8 columns d, the 4-key run at position
 // perm16(4 kg) of row d (8 bytes; the 16 threads of one dc fill each row segment).
 // Keys past Sk and columns past D are written as zeros.
+// Each block first derives the exponents (tbf16/attention.py:267-277) from the
+// per-head partial maxima: a from all q and k heads, ev of its own kv head;
+// blocks (0, bhk) store them (a by block (0, 0)) to the workspace and to the
+// caller's exps, where the forward kernel and the backward read them.
 template <int DP>
 __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
   constexpr int CPR = DP / 8;
+  __shared__ int red[4];
   const int bhk = blockIdx.y, b = bhk / p.Hkv, hk = bhk % p.Hkv;
   const int key0 = blockIdx.x * BKV;
-  const int a = p.ex[0], ev = p.ex[2 + bhk];
+  int eq = INT_MIN, ek = INT_MIN;
+  heads_max(p.part_q, p.B * p.H, p.nch_q, [&](int, float m) { eq = max(eq, frexp_exp(m)); });
+  heads_max(p.part_k, p.B * p.Hkv, p.nch_k, [&](int, float m) { ek = max(ek, frexp_exp(m)); });
+  eq = block_max_int<256>(eq, red);
+  ek = block_max_int<256>(ek, red);
+  int a = (ek - eq) >> 1;  // floor division
+  a = max(min(a, 14 - eq), ek - 14);
+  float mv = 0.f;
+  for (int c = threadIdx.x; c < p.nch_v; c += 256) mv = fmaxf(mv, p.part_v[bhk * p.nch_v + c]);
+  mv = wave_max(mv);
+  __syncthreads();  // red is reused
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = __float_as_int(mv);  // non-negative: int order = float order
+  __syncthreads();
+  const int ev = frexp_exp(__int_as_float(max(max(red[0], red[1]), max(red[2], red[3])))) - p.v_exp;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    p.ex[2 + bhk] = ev;
+    if (p.exps) p.exps[2 + bhk] = ev;
+    if (bhk == 0) {
+      p.ex[0] = a;
+      p.ex[1] = 0;
+      if (p.exps) {
+        p.exps[0] = a;
+        p.exps[1] = 0;
+      }
+    }
+  }
   const float sk = ldexp1(-a), sv = ldexp1(-ev);
   const uint16_t* kb = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
   const uint16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
@@ -236,7 +252,7 @@ attn_fwd_kernel(FwdParams p) {
   const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
   const int hk = h / (p.H / p.Hkv);
 
-  // ---- exponents (finalised by attn_exps_kernel) ----
+  // ---- exponents (derived by kv_prep_kernel) ----
   const int a = p.ex[0];
   const int ev = p.ex[2 + b * p.Hkv + hk];
   const float sq = ldexp1(a);
@@ -553,15 +569,18 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   float* pq = reinterpret_cast<float*>(ws);
   float* pk = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_k);
   float* pv = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_v);
-  if (int rc = launch_head_amax_partial(q, TBF16_DT_BF16, B, H, Sq, D, q_strides[0], q_strides[1], q_strides[2], pq,
-                                        w.nch_q, st))
-    return rc;
-  if (int rc = launch_head_amax_partial(k, TBF16_DT_BF16, B, Hkv, Sk, D, k_strides[0], k_strides[1], k_strides[2],
-                                        pk, w.nch_k, st))
-    return rc;
-  if (int rc = launch_head_amax_partial(v, TBF16_DT_BF16, B, Hkv, Sk, D, v_strides[0], v_strides[1], v_strides[2],
-                                        pv, w.nch_v, st))
-    return rc;
+  {
+    // partial per-head maxima of q, k and v in one launch
+    AmaxSegs segs;
+    segs.n = 3;
+    segs.seg[0] = AmaxSeg{(const uint16_t*)q, B * H, H, Sq, q_strides[0], q_strides[1], q_strides[2],
+                          cdiv(Sq, w.nch_q), w.nch_q, pq};
+    segs.seg[1] = AmaxSeg{(const uint16_t*)k, B * Hkv, Hkv, Sk, k_strides[0], k_strides[1], k_strides[2],
+                          cdiv(Sk, w.nch_k), w.nch_k, pk};
+    segs.seg[2] = AmaxSeg{(const uint16_t*)v, B * Hkv, Hkv, Sk, v_strides[0], v_strides[1], v_strides[2],
+                          cdiv(Sk, w.nch_v), w.nch_v, pv};
+    if (int rc = launch_head_amax3(segs, D, st)) return rc;
+  }
   FwdParams p;
   p.q = (const uint16_t*)q;
   p.k = (const uint16_t*)k;
@@ -589,8 +608,6 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   p.vt16 = reinterpret_cast<uint16_t*>(wsb + w.off_vt16);
   p.Skp = (int)w.Skp;
   p.DPc = (int)w.DP;
-  attn_exps_kernel<<<1, 256, 0, st>>>(p);
-  TB_LAUNCH_CHECK("attn_fwd/exps");
   {
     const dim3 g((unsigned)(w.Skp / BKV), (unsigned)(B * Hkv));
     if (w.DP == 64) kv_prep_kernel<64><<<g, 256, 0, st>>>(p);

@@ -76,12 +76,28 @@ __device__ __forceinline__ int ev_of(const BwdParams& p, int b, int h) {
 }
 
 // e = max over (b, h) of frexp(amax dO[b,h]) + ev_q[b,h]  (block-wide)
+// (wave-parallel: wave w reduces heads w, w + 4, ..., a lane per chunk, eight
+// heads' loads in flight before any is reduced)
 __device__ int compute_e(const BwdParams& p, int* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nbh = p.B * p.H, nch = p.nch_do;
   int e = INT_MIN;
-  for (int bh = threadIdx.x; bh < p.B * p.H; bh += NTH) {
-    float m = 0.f;
-    for (int c = 0; c < p.nch_do; ++c) m = fmaxf(m, p.part_do[bh * p.nch_do + c]);
-    e = max(e, frexp_exp(m) + ev_of(p, bh / p.H, bh % p.H));
+  for (int bh0 = wave; bh0 < nbh; bh0 += 32) {
+    float m[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m[j] = 0.f;
+    for (int c = lane; c < nch; c += 64) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int bh = bh0 + 4 * j;
+        if (bh < nbh) m[j] = fmaxf(m[j], p.part_do[bh * nch + c]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int bh = bh0 + 4 * j;
+      const float mx = wave_max(m[j]);
+      if (bh < nbh) e = max(e, frexp_exp(mx) + ev_of(p, bh / p.H, bh % p.H));
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) e = max(e, __shfl_xor(e, o, 64));

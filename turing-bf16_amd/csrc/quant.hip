@@ -166,25 +166,56 @@ __device__ __forceinline__ float amax8<_Float16>(uint4 v) {  // fp16
                fmaxf(fmaxf(fabsf(f16_lo(v.z)), fabsf(f16_hi(v.z))), fmaxf(fabsf(f16_lo(v.w)), fabsf(f16_hi(v.w)))));
 }
 
+// max |x| over rows [chunk * rows_per_chunk, ...) of head (b, h) of a (B, H, S, D)
+// tensor, block-wide, into partial[bh * nchunks + chunk]
+template <typename T>
+__device__ __forceinline__ void head_amax_block(const uint16_t* __restrict__ x, int64_t bh, int64_t H, int64_t S,
+                                                int64_t D, int64_t sb, int64_t sh, int64_t ss, int64_t rows_per_chunk,
+                                                int64_t nchunks, int64_t chunk, float* __restrict__ partial) {
+  const int64_t b = bh / H, h = bh % H;
+  const int64_t s0 = chunk * rows_per_chunk, s1 = min(S, s0 + rows_per_chunk);
+  const uint16_t* base = x + b * sb + h * sh + s0 * ss;
+  const int D8 = (int)(D >> 3), n = (int)((s1 - s0) * D8);
+  // four loads in flight per thread before any of them is reduced
+  float m0 = 0.f, m1 = 0.f;
+  int i = threadIdx.x;
+  for (; i + 3 * 256 < n; i += 4 * 256) {
+    uint4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ij = i + j * 256;
+      v[j] = ldg16(base + (int64_t)(ij / D8) * ss + (ij % D8) * 8);
+    }
+    m0 = fmaxf(m0, fmaxf(amax8<T>(v[0]), amax8<T>(v[1])));
+    m1 = fmaxf(m1, fmaxf(amax8<T>(v[2]), amax8<T>(v[3])));
+  }
+  for (; i < n; i += 256) m0 = fmaxf(m0, amax8<T>(ldg16(base + (int64_t)(i / D8) * ss + (i % D8) * 8)));
+  float m = fmaxf(m0, m1);
+  __shared__ float red[4];
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[bh * nchunks + chunk] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void head_amax_partial_kernel(const uint16_t* __restrict__ x, int64_t H, int64_t S,
                                                                 int64_t D, int64_t sb, int64_t sh, int64_t ss,
                                                                 int64_t rows_per_chunk, int64_t nchunks,
                                                                 float* __restrict__ partial) {
-  const int64_t bh = blockIdx.x, b = bh / H, h = bh % H;
-  const int64_t s0 = (int64_t)blockIdx.y * rows_per_chunk, s1 = min(S, s0 + rows_per_chunk);
-  const uint16_t* base = x + b * sb + h * sh;
-  const int64_t D8 = D >> 3, n = (s1 - s0) * D8;
-  float m = 0.f;
-  for (int64_t i = threadIdx.x; i < n; i += 256) {
-    const int64_t s = s0 + i / D8, d = (i % D8) * 8;
-    m = fmaxf(m, amax8<T>(ldg16(base + s * ss + d)));
-  }
-  __shared__ float red[4];
-  m = wave_max(m);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) partial[bh * nchunks + blockIdx.y] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  head_amax_block<T>(x, blockIdx.x, H, S, D, sb, sh, ss, rows_per_chunk, nchunks, blockIdx.y, partial);
+}
+
+// The same for up to three bf16 tensors in one launch: block x runs over the
+// tensors' heads end to end, block y over chunks (past a tensor's own count the
+// block has nothing to do).
+__global__ __launch_bounds__(256) void head_amax3_kernel(AmaxSegs segs, int64_t D) {
+  int64_t bh = blockIdx.x;
+  int s = 0;
+  while (s + 1 < segs.n && bh >= segs.seg[s].BH) bh -= segs.seg[s++].BH;
+  const AmaxSeg& g = segs.seg[s];
+  if ((int64_t)blockIdx.y >= g.nch) return;
+  head_amax_block<uint16_t>(g.x, bh, g.H, g.S, D, g.sb, g.sh, g.ss, g.rows, g.nch, blockIdx.y, g.partial);
 }
 
 __global__ void reduce_partials_kernel(const float* __restrict__ partial, int64_t n, int64_t nchunks,
@@ -290,6 +321,18 @@ int64_t head_chunks(int64_t BH, int64_t S) {
 // Shared with attention.hip: partial head maxima in one launch per tensor.
 namespace tbf16 {
 int64_t head_amax_chunks(int64_t BH, int64_t S) { return head_chunks(BH, S); }
+
+int launch_head_amax3(const AmaxSegs& segs, int64_t D, hipStream_t st) {
+  int64_t bhs = 0, nch = 0;
+  for (int i = 0; i < segs.n; ++i) {
+    bhs += segs.seg[i].BH;
+    nch = std::max(nch, segs.seg[i].nch);
+  }
+  if (bhs == 0) return 0;
+  head_amax3_kernel<<<dim3((unsigned)bhs, (unsigned)nch), 256, 0, st>>>(segs, D);
+  TB_LAUNCH_CHECK("head_amax3");
+  return 0;
+}
 
 int launch_head_amax_partial(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
                              int64_t sh, int64_t ss, float* partial, int64_t nchunks, hipStream_t st) {
