@@ -249,7 +249,9 @@ attn_fwd_kernel(FwdParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, fk = lane >> 5;
-  const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
+  // grid (heads, query blocks): dispatch runs over heads first, so the heaviest
+  // query blocks of every head (causal) go out before any lighter one
+  const int bh = blockIdx.x, b = bh / p.H, h = bh % p.H;
   const int hk = h / (p.H / p.Hkv);
 
   // ---- exponents (derived by kv_prep_kernel) ----
@@ -260,10 +262,10 @@ attn_fwd_kernel(FwdParams p) {
   // Query tiles of this block: one, or with pair (causal) the heavy tile
   // ntiles-1-x and then the light tile x, so every block does the same work.
   const int ntiles = (p.Sq + BQW - 1) / BQW;
-  const int bx = (int)blockIdx.x;
+  const int bx = (int)blockIdx.y;
   const int npass = (CAUSAL && p.pair) ? (bx == ntiles - 1 - bx ? 1 : 2) : 1;
   for (int pass = 0; pass < npass; ++pass) {
-    const int qt = !CAUSAL ? bx : p.pair ? (pass == 0 ? ntiles - 1 - bx : bx) : (int)gridDim.x - 1 - bx;
+    const int qt = !CAUSAL ? bx : p.pair ? (pass == 0 ? ntiles - 1 - bx : bx) : (int)gridDim.y - 1 - bx;
     const int q0 = qt * BQW;
     // ---- Q fragments in registers (fp16, scaled by 2^a) ----
     const int qrow = q0 + wave * 32 + fr;
@@ -526,7 +528,7 @@ int launch_fwd_dp(FwdParams p, bool causal, bool has_bias, hipStream_t st, int n
   if (DP > 128) nw = 4;
   const int64_t ntiles = cdiv(p.Sq, nw == 8 ? 256 : 128);
   p.pair = pair && nw == 4;
-  const dim3 grid((unsigned)(p.pair ? cdiv(ntiles, 2) : ntiles), p.B * p.H);
+  const dim3 grid(p.B * p.H, (unsigned)(p.pair ? cdiv(ntiles, 2) : ntiles));
   if (nw == 8) {
     if constexpr (DP <= 128) return launch_fwd_nw<DP, 8, 2>(p, causal, has_bias, grid, st);
   }

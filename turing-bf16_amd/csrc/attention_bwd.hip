@@ -205,8 +205,10 @@ dkdv_kernel(BwdParams p) {
   __shared__ __align__(16) float s_delta[2][BQ];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, fr = lane & 31, fk = lane >> 5;
-  const int bk = blockIdx.y, b = bk / p.Hkv, hk = bk % p.Hkv;
-  const int k0 = blockIdx.x * BK;
+  // grid (heads, key blocks): dispatch runs over heads first, so every head's
+  // heaviest key blocks (the most query tiles under a causal mask) go out first
+  const int bk = blockIdx.x, b = bk / p.Hkv, hk = bk % p.Hkv;
+  const int k0 = blockIdx.y * BK;
   const int a = p.exps_fwd[0];
   const int ev = p.exps_fwd[2 + bk];
   const int G = p.exps_out[1];
@@ -430,8 +432,9 @@ dq_kernel(BwdParams p) {
   uint8_t* sV = smem + TILE;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, fr = lane & 31, fk = lane >> 5;
-  const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H, hk = h / (p.H / p.Hkv);
-  const int qt = CAUSAL ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;
+  // grid (heads, query blocks), heaviest query blocks of every head first
+  const int bh = blockIdx.x, b = bh / p.H, h = bh % p.H, hk = h / (p.H / p.Hkv);
+  const int qt = CAUSAL ? (int)(gridDim.y - 1 - blockIdx.y) : (int)blockIdx.y;
   const int q0 = qt * BQ;
   const int a = p.exps_fwd[0];
   const int ev = p.exps_fwd[2 + b * p.Hkv + hk];
@@ -609,8 +612,8 @@ BwdWs bwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t 
 
 template <int DP>
 int launch_bwd_dp(const BwdParams& p, bool causal, bool has_bias, hipStream_t st) {
-  dim3 g_kv((unsigned)cdiv(p.Sk, 128), (unsigned)(p.B * p.Hkv));
-  dim3 g_q((unsigned)cdiv(p.Sq, 128), (unsigned)(p.B * p.H));
+  dim3 g_kv((unsigned)(p.B * p.Hkv), (unsigned)cdiv(p.Sk, 128));
+  dim3 g_q((unsigned)(p.B * p.H), (unsigned)cdiv(p.Sq, 128));
 #define LAUNCH(C, HB)                                  \
   dkdv_kernel<DP, C, HB><<<g_kv, NTH, 0, st>>>(p);     \
   TB_LAUNCH_CHECK("attn_bwd/dkdv");                    \
