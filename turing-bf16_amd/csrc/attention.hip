@@ -33,6 +33,8 @@
 #include <algorithm>
 #include <math.h>
 
+#include <type_traits>
+
 #include "abi_util.h"
 #include "common.h"
 
@@ -233,21 +235,23 @@ attn_fwd_kernel(FwdParams p) {
   constexpr int KS = DP / 16;            // MFMA k-steps over the head dim
   constexpr int DB = DP / 32;            // 32-wide d blocks of O^T
   constexpr int CPR = DP / 8;            // 16-byte chunks per K row
-  constexpr int KTH = NW == 8 ? NT / 2 : NT;  // threads staging K
-  constexpr int VTH = NW == 8 ? NT / 2 : NT;  // threads staging V
-  constexpr int VT0 = NW == 8 ? NT / 2 : 0;   // first V-staging thread
-  constexpr int KL = BKV * CPR / KTH;         // K chunks per staging thread
-  constexpr int VL = DP * 8 / VTH;            // V^T chunks (8 per row of 64 keys)
-  static_assert(KL * KTH == BKV * CPR && VL * VTH == DP * 8, "K/V staging");
-  // one staging array shared by the K and V roles: [K chunks][V^T chunks]
-  constexpr int VOFF = NW == 8 ? 0 : KL;
-  constexpr int SL = NW == 8 ? (KL > VL ? KL : VL) : KL + VL;
   constexpr int KBYTES = BKV * DP * 2;
   constexpr int STAGE = KBYTES + DP * 128;
-  __shared__ __align__(16) uint8_t smem[2 * STAGE];
+  // V^T fragments read during the QK product (registers allow it up to DP = 128
+  // without the bias rows)
+  constexpr bool VPRE = DP <= 128 && !HAS_BIAS;
+  // K and V^T tiles go global -> LDS directly, 1 KB per wave instruction: BPW
+  // such blocks per wave per tile, the first KPW of them K, the rest V^T
+  constexpr int KBLK = KBYTES / 1024, NBLK = STAGE / 1024;
+  static_assert(NBLK % NW == 0 && KBLK % NW == 0, "K/V staging blocks");
+  constexpr int BPW = NBLK / NW, KPW = KBLK / NW;
+  // two stages as separate objects, so that the compiler's LDS alias analysis
+  // sees that reads of one stage never wait for the loads into the other
+  __shared__ __align__(1024) uint8_t smem0[STAGE];
+  __shared__ __align__(1024) uint8_t smem1[STAGE];
   __shared__ int red[NW];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fk = lane >> 5;
   // grid (heads, query blocks): dispatch runs over heads first, so the heaviest
   // query blocks of every head (causal) go out before any lighter one
@@ -281,46 +285,35 @@ attn_fwd_kernel(FwdParams p) {
       }
     }
 
-    // ---- K / V^T staging: plain 16-byte copies of the workspace's converted tiles ----
+    // ---- K / V^T staging: the workspace's converted tiles copied global -> LDS ----
+    // Lane j of a wave instruction lands at byte 16 j of its 1 KB block, so the
+    // row swizzle is applied on the source side: the lane fetches the logical
+    // chunk that belongs at its LDS position. Block bi of a stage: K rows
+    // (bi * 1024 / (2 DP) ...) for bi < KBLK, else V^T rows d.
     const int bhk = b * p.Hkv + hk;
     const BufRes kres = make_res(p.k16 + (int64_t)bhk * p.Skp * DP, min<int64_t>((int64_t)p.Skp * DP * 2, 0x7fffffff));
     const BufRes vres = make_res(p.vt16 + (int64_t)bhk * DP * p.Skp, min<int64_t>((int64_t)DP * p.Skp * 2, 0x7fffffff));
-    const bool k_stager = NW != 8 || tid < KTH;
-    const bool v_stager = NW != 8 || tid >= VT0;
-    const int ktid = tid, vtid = tid - VT0;
-    uint4 st[PF][SL];
-    auto gload = [&](uint4(&sr)[SL], int kb) {
-      if (k_stager) {
+    int voff[BPW];
   #pragma unroll
-        for (int i = 0; i < KL; ++i) {
-          const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
-          sr[i] = buf_load16(kres, (row * DP + ch * 8) * 2, kb * BKV * DP * 2);
-        }
+    for (int i = 0; i < BPW; ++i) {
+      const int bi = wave + NW * i;
+      if (i < KPW) {
+        const int byte = bi * 1024 + 16 * lane, row = byte / (2 * DP), phys = (byte % (2 * DP)) >> 4;
+        const int lch = (swz_k<DP>(row, phys) - row * 2 * DP) >> 4;  // the XOR swizzle is its own inverse
+        voff[i] = (row * DP + lch * 8) * 2;
+      } else {
+        const int byte = (bi - KBLK) * 1024 + 16 * lane, d = byte >> 7, phys = (byte & 127) >> 4;
+        const int ch = (swz_vt(d, phys) - d * 128) >> 4;
+        voff[i] = (d * p.Skp + ch * 8) * 2;
       }
-      if (v_stager) {
+    }
+    auto dload = [&](uint8_t* stage, int kb) {
+      const uint32_t base = lds_addr(stage);
   #pragma unroll
-        for (int i = 0; i < VL; ++i) {
-          const int c = vtid + i * VTH, d = c >> 3, ch = c & 7;
-          sr[VOFF + i] = buf_load16(vres, (d * p.Skp + ch * 8) * 2, kb * BKV * 2);
-        }
-      }
-    };
-    auto lstore = [&](const uint4(&sr)[SL], int stg) {
-      uint8_t* sK = smem + stg * STAGE;
-      uint8_t* sV = sK + KBYTES;
-      if (k_stager) {
-  #pragma unroll
-        for (int i = 0; i < KL; ++i) {
-          const int c = ktid + i * KTH, row = c / CPR, ch = c % CPR;
-          *reinterpret_cast<uint4*>(sK + swz_k<DP>(row, ch)) = sr[i];
-        }
-      }
-      if (v_stager) {
-  #pragma unroll
-        for (int i = 0; i < VL; ++i) {
-          const int c = vtid + i * VTH, d = c >> 3, ch = c & 7;
-          *reinterpret_cast<uint4*>(sV + swz_vt(d, ch)) = sr[VOFF + i];
-        }
+      for (int i = 0; i < BPW; ++i) {
+        const uint32_t dst = base + (wave + NW * i) * 1024;
+        if (i < KPW) buf_load16_lds(kres, dst, voff[i], kb * BKV * DP * 2);
+        else buf_load16_lds(vres, dst, voff[i], kb * BKV * 2);
       }
     };
 
@@ -341,20 +334,77 @@ attn_fwd_kernel(FwdParams p) {
     if constexpr (HAS_BIAS)
       brow = p.bias + (int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh + (int64_t)min(qrow, p.Sq - 1) * p.bias_sq;
 
-    auto step = [&](int kb) {
-      const uint8_t* sK = smem + (kb & 1) * STAGE;
+    // The last PV step of each tile runs at the start of the next tile, after its
+    // first K reads have gone out (its fragments were read before the barrier),
+    // so the barrier's drain and those reads' latency hide behind 4 MFMAs. It
+    // starts as zeros (adds nothing) and is flushed after the last tile.
+    half8 dpf, dvf[DB];
+    for (int e = 0; e < 8; ++e) dpf[e] = (_Float16)0.f;
+  #pragma unroll
+    for (int db = 0; db < DB; ++db) dvf[db] = dpf;
+    auto deferred = [&]() {
+  #pragma unroll
+      for (int db = 0; db < DB; ++db) acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(dvf[db], dpf, acc_o[db], 0, 0, 0);
+    };
+    auto step = [&](int kb, const uint8_t* sK, auto masked_c) {
+      constexpr bool MASKED = decltype(masked_c)::value;
       const uint8_t* sV = sK + KBYTES;
-      // S^T = K Q^T for two 32-key halves: lane = one query row, 16 keys each
+      // S^T = K Q^T for two 32-key halves: lane = one query row, 16 keys each.
+      // Fragment reads run ahead of their MFMAs (the compiler otherwise reads each
+      // fragment at its use and waits on it): the first half's K fragments, then
+      // the second half's K fragments between the first half's MFMAs, then the V^T
+      // fragments of the first two PV steps between the second half's MFMAs; the
+      // remaining V^T fragments are read during the PV MFMAs two steps ahead.
+      // Pinned by instruction-group schedules (DP <= 128 without bias rows; else
+      // each fragment is read at its use).
       floatx16 sacc[2];
   #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
+      for (int kh = 0; kh < 2; ++kh)
   #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[kh][r] = 0.f;
+      auto kread = [&](int kh, int s) {
+        return *reinterpret_cast<const half8*>(sK + swz_k<DP>(kh * 32 + fr, 2 * s + fk));
+      };
+      auto vread = [&](int ks, int db) {
+        return *reinterpret_cast<const half8*>(sV + swz_vt(db * 32 + fr, 2 * ks + fk));
+      };
+      half8 vf[4][DB];
+      if constexpr (VPRE) {
+        half8 kf[2][KS];
+  #pragma unroll
+        for (int s = 0; s < KS; ++s) kf[0][s] = kread(0, s);
+        deferred();
   #pragma unroll
         for (int s = 0; s < KS; ++s) {
-          const half8 kf = *reinterpret_cast<const half8*>(sK + swz_k<DP>(kh * 32 + fr, 2 * s + fk));
-          sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], sacc[kh], 0, 0, 0);
+          sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][s], qf[s], sacc[0], 0, 0, 0);
+          kf[1][s] = kread(1, s);
         }
+  #pragma unroll
+        for (int s = 0; s < KS; ++s) sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[1][s], qf[s], sacc[1], 0, 0, 0);
+  #pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+  #pragma unroll
+          for (int db = 0; db < DB; ++db) vf[ks][db] = vread(ks, db);
+        constexpr int VR = (2 * DB + KS - 1) / KS;  // V^T reads per MFMA of the second half
+        __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, DB, 0);  // the previous tile's deferred step
+  #pragma unroll
+        for (int i = 0; i < KS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+  #pragma unroll
+        for (int i = 0; i < KS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (i * VR < 2 * DB) __builtin_amdgcn_sched_group_barrier(0x100, VR, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        deferred();
+  #pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+  #pragma unroll
+          for (int s = 0; s < KS; ++s) sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kread(kh, s), qf[s], sacc[kh], 0, 0, 0);
       }
       const int key0 = kb * BKV;
       const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0 + wave * 32);
@@ -368,13 +418,13 @@ attn_fwd_kernel(FwdParams p) {
                           (key < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[key]) * kLog2e : 0.f);
           }
       }
-      if (edge) mask_tile(sacc, key0, p.Sk, CAUSAL ? qrow : INT_MAX, fk);
+      if (MASKED && edge) mask_tile(sacc, key0, p.Sk, CAUSAL ? qrow : INT_MAX, fk);
       float mx = -INFINITY;
   #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
   #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kh][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+      mx = max_xor32(mx) * c;
       if (__any(mx > m_run + 8.f)) {  // wave-uniform: rescale O and l only when some row needs it
         const float m_new = fmaxf(m_run, mx);
         const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -406,47 +456,56 @@ attn_fwd_kernel(FwdParams p) {
         const uint4 pw = make_uint4(pk[ks >> 1][4 * (ks & 1) + 0], pk[ks >> 1][4 * (ks & 1) + 1],
                                     pk[ks >> 1][4 * (ks & 1) + 2], pk[ks >> 1][4 * (ks & 1) + 3]);
         const half8 pf = __builtin_bit_cast(half8, pw);
+        if (ks == 3) {  // deferred past the barrier (operands stay in registers)
+          dpf = pf;
   #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const half8 vf = *reinterpret_cast<const half8*>(sV + swz_vt(db * 32 + fr, 2 * ks + fk));
-          acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, acc_o[db], 0, 0, 0);
+          for (int db = 0; db < DB; ++db) dvf[db] = VPRE ? vf[3][db] : vread(3, db);
+        } else if constexpr (VPRE) {
+  #pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[ks][db], pf, acc_o[db], 0, 0, 0);
+            if (ks < 2) vf[ks + 2][db] = vread(ks + 2, db);
+          }
+        } else {
+  #pragma unroll
+          for (int db = 0; db < DB; ++db) acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vread(ks, db), pf, acc_o[db], 0, 0, 0);
         }
       }
     };
 
-    // Pipeline as in the GEMM: LDS stage kb % 2 holds tile kb, register set u holds
-    // the tile congruent to u mod PF; the steady state issues its loads
-    // unconditionally so the younger sets stay in flight.
-  #pragma unroll
-    for (int i = 0; i < PF; ++i)
-      if (i < nkb) gload(st[i], i);
-    if (nkb > 0) lstore(st[0], 0);
-    __syncthreads();
-    int kb0 = 0;
-    for (; kb0 + 2 * PF - 1 < nkb; kb0 += PF) {
-  #pragma unroll
-      for (int u = 0; u < PF; ++u) {
-        gload(st[u], kb0 + u + PF);
-        step(kb0 + u);
-        lstore(st[(u + 1) % PF], (kb0 + u + 1) & 1);
+    // Tile kb lives in stage kb % 2; tile kb + 1's loads go out when tile kb's
+    // computation starts (its stage was last read before the previous barrier)
+    // and are waited for at the barrier that ends tile kb. Tiles [0, nfull) are
+    // whole for every wave of the block; the rest (the diagonal, the end of the
+    // keys) run in a second loop with the masking compiled in (nfull is even, so
+    // both loops start on stage 0).
+    int nfull = min(nkb, p.Sk / BKV);
+    if constexpr (CAUSAL) nfull = min(nfull, (q0 + 1) / BKV);
+    nfull &= ~1;
+    auto tiles = [&](int kb_begin, int kb_end, auto masked_c) {
+      auto run = [&](int kb, const uint8_t* sK) { step(kb, sK, masked_c); };
+      for (int kb = kb_begin; kb < kb_end; kb += 2) {
+        if (kb + 1 < nkb) dload(smem1, kb + 1);
+        run(kb, smem0);
+        wait_vmem();
         __syncthreads();
-      }
-    }
-    for (; kb0 < nkb; kb0 += PF) {
-  #pragma unroll
-      for (int u = 0; u < PF; ++u) {
-        const int kb = kb0 + u;
-        if (kb < nkb) {
-          if (kb + PF < nkb) gload(st[u], kb + PF);
-          step(kb);
-          if (kb + 1 < nkb) lstore(st[(u + 1) % PF], (kb + 1) & 1);
+        if (kb + 1 < kb_end) {
+          if (kb + 2 < nkb) dload(smem0, kb + 2);
+          run(kb + 1, smem1);
+          wait_vmem();
           __syncthreads();
         }
       }
-    }
+    };
+    if (nkb > 0) dload(smem0, 0);
+    wait_vmem();
+    __syncthreads();
+    tiles(0, nfull, std::false_type{});
+    tiles(nfull, nkb, std::true_type{});
+    deferred();
 
     // ---- epilogue ----
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float l_tot = sum_xor32(l_run);
     if (qrow < p.Sq) {
     const float sev = ldexp1(ev);
     const int64_t orow = ((int64_t)bh * p.Sq + qrow) * p.D;

@@ -157,6 +157,44 @@ __device__ __forceinline__ uint4 buf_load16(BufRes r, int voffset, int soffset) 
   return __builtin_bit_cast(uint4, raw_buffer_load_b128(d, voffset, __builtin_amdgcn_readfirstlane(soffset), 0));
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ void raw_buffer_load_lds(int4v rsrc, lds_void* lds, int size, int voffset, int soffset, int offset,
+                                    int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+// 16-byte buffer load straight into LDS (gfx950 buffer_load_dwordx4 ... lds): the
+// wave's 64 lanes fill the 1 KB at lds_byte (a wave-uniform LDS byte address),
+// lane j's 16 bytes at lds_byte + 16 j (established on the device). No VGPRs
+// hold the data; the caller waits with wait_vmem() before the barrier that
+// publishes the LDS region.
+__device__ __forceinline__ void buf_load16_lds(BufRes r, uint32_t lds_byte, int voffset, int soffset) {
+  int4v d;
+  d.x = __builtin_amdgcn_readfirstlane(r.lo);
+  d.y = __builtin_amdgcn_readfirstlane(r.hi);
+  d.z = __builtin_amdgcn_readfirstlane(r.bytes);
+  d.w = 0x00020000;
+  raw_buffer_load_lds(d, (lds_void*)(uintptr_t)__builtin_amdgcn_readfirstlane(lds_byte), 16, voffset,
+                      __builtin_amdgcn_readfirstlane(soffset), 0, 0);
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// LDS byte address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void*)p;
+}
+
+// Values of lanes l and l ^ 32 combined, through v_permlane32_swap (gfx950: a
+// VALU exchange of the wave's two 32-lane halves, no LDS round trip). Both
+// results of the swap hold one of the two lanes' values, so a symmetric op
+// (max, sum) needs no knowledge of which is which.
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ---- LDS tiles ---------------------------------------------------------------
 
 // Byte offset of 16-byte chunk `chunk` of row `row` in a row-major DP-wide fp16 LDS
