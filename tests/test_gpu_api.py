@@ -185,7 +185,8 @@ def _check(out, r):
     assert out.dtype == torch.bfloat16 and torch.isfinite(out).all() and err < 1e-2, err
 
 
-@pytest.mark.parametrize("B,H,Sq,Skv,D", [(2, 24, 1024, 1024, 64), (2, 20, 1024, 300, 112), (1, 12, 3200, 512, 128)])
+@pytest.mark.parametrize("B,H,Sq,Skv,D", [(2, 24, 1024, 1024, 64), (2, 20, 1024, 300, 112), (1, 12, 3200, 512, 128),
+                                          (1, 4, 700, 640, 256)])
 def test_sdpa_api_masks_and_layouts(dev, B, H, Sq, Skv, D):
     convert = importlib.import_module("tbf16.convert")
     tbf16.install_sdpa()

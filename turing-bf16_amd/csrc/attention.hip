@@ -8,8 +8,9 @@
 // k16 = k * 2^-a and v16 = v * 2^-ev (exact powers of two) to the workspace as
 // fp16, k16 row-major (B, Hkv, Skp, DP) and v16 transposed (B, Hkv, DP, Skp) with
 // keys permuted as the PV operand wants them, both zero-padded, so the forward
-// kernel stages K and V tiles as plain copies: each K/V element is converted once
-// instead of once per query block. q16 = q * 2^a is converted on the fly (once per
+// kernel copies K and V tiles global -> LDS directly (buffer_load ... lds, no
+// registers in between): each K/V element is converted once instead of once per
+// query block. q16 = q * 2^a is converted on the fly (once per
 // row).
 //
 // Block = 4 or 8 waves, 32 query rows per wave; key tiles of 64.
@@ -26,8 +27,8 @@
 //  - output bf16(O / l * 2^ev) written from registers: one rounding.
 // Causal blocks are launched heaviest first, or (few blocks per CU) each takes a
 // heavy and a light query tile; key tiles past the diagonal are skipped, and
-// only tiles crossing the diagonal or the end of the keys take the
-// (wave-uniform) masking branch.
+// only tiles crossing the diagonal or the end of the keys run the masked copy of
+// the tile loop.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -224,11 +225,10 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
   }
 }
 
-// Forward kernel: NW waves, 32 query rows each (BQ = 32 * NW), 64-key tiles.
-// NW = 8 (two waves per SIMD, K/V conversion shared by 256 queries): waves 0-3
-// stage K, waves 4-7 stage V^T. NW = 4: every thread stages both. PF register
-// sets of prefetched K/V tiles.
-template <int DP, int NW, int PF, bool CAUSAL, bool HAS_BIAS>
+// Forward kernel: NW waves, 32 query rows each (BQ = 32 * NW), 64-key tiles
+// staged in two LDS stages by direct global -> LDS loads shared out over all
+// waves. NW = 8: two waves per SIMD, one block per CU; NW = 4: two blocks per CU.
+template <int DP, int NW, bool CAUSAL, bool HAS_BIAS>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(DP > 128 ? 1 : 2, DP > 128 ? 1 : 2))) void
 attn_fwd_kernel(FwdParams p) {
   constexpr int NT = NW * 64, BQW = 32 * NW;
@@ -246,7 +246,8 @@ attn_fwd_kernel(FwdParams p) {
   static_assert(NBLK % NW == 0 && KBLK % NW == 0, "K/V staging blocks");
   constexpr int BPW = NBLK / NW, KPW = KBLK / NW;
   // two stages as separate objects, so that the compiler's LDS alias analysis
-  // sees that reads of one stage never wait for the loads into the other
+  // sees that reads of one stage never wait for the loads into the other (a
+  // third stage, loads two tiles ahead, measured no faster)
   __shared__ __align__(1024) uint8_t smem0[STAGE];
   __shared__ __align__(1024) uint8_t smem1[STAGE];
   __shared__ int red[NW];
@@ -368,7 +369,7 @@ attn_fwd_kernel(FwdParams p) {
       auto vread = [&](int ks, int db) {
         return *reinterpret_cast<const half8*>(sV + swz_vt(db * 32 + fr, 2 * ks + fk));
       };
-      half8 vf[4][DB];
+      half8 vf[VPRE ? 4 : 1][DB];
       if constexpr (VPRE) {
         half8 kf[2][KS];
   #pragma unroll
@@ -459,7 +460,10 @@ attn_fwd_kernel(FwdParams p) {
         if (ks == 3) {  // deferred past the barrier (operands stay in registers)
           dpf = pf;
   #pragma unroll
-          for (int db = 0; db < DB; ++db) dvf[db] = VPRE ? vf[3][db] : vread(3, db);
+          for (int db = 0; db < DB; ++db) {
+            if constexpr (VPRE) dvf[db] = vf[3][db];
+            else dvf[db] = vread(3, db);
+          }
         } else if constexpr (VPRE) {
   #pragma unroll
           for (int db = 0; db < DB; ++db) {
@@ -483,25 +487,25 @@ attn_fwd_kernel(FwdParams p) {
     if constexpr (CAUSAL) nfull = min(nfull, (q0 + 1) / BKV);
     nfull &= ~1;
     auto tiles = [&](int kb_begin, int kb_end, auto masked_c) {
-      auto run = [&](int kb, const uint8_t* sK) { step(kb, sK, masked_c); };
-      for (int kb = kb_begin; kb < kb_end; kb += 2) {
-        if (kb + 1 < nkb) dload(smem1, kb + 1);
-        run(kb, smem0);
+      // tile kb from stage cur; tile kb + 1 loads into stage nxt
+      auto one = [&](int kb, const uint8_t* cur, uint8_t* nxt) {
+        if (kb + 1 < nkb) dload(nxt, kb + 1);
+        step(kb, cur, masked_c);
         wait_vmem();
         __syncthreads();
-        if (kb + 1 < kb_end) {
-          if (kb + 2 < nkb) dload(smem0, kb + 2);
-          run(kb + 1, smem1);
-          wait_vmem();
-          __syncthreads();
-        }
+      };
+      for (int kb = kb_begin; kb < kb_end; kb += 2) {
+        one(kb, smem0, smem1);
+        if (kb + 1 < kb_end) one(kb + 1, smem1, smem0);
       }
     };
     if (nkb > 0) dload(smem0, 0);
     wait_vmem();
     __syncthreads();
-    tiles(0, nfull, std::false_type{});
-    tiles(nfull, nkb, std::true_type{});
+    // (without the fragment prefetch, one loop with the masking branch keeps the
+    // register allocation within bounds)
+    if constexpr (VPRE) tiles(0, nfull, std::false_type{});
+    tiles(VPRE ? nfull : 0, nkb, std::true_type{});
     deferred();
 
     // ---- epilogue ----
@@ -555,43 +559,43 @@ WsLayout fwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64
   return w;
 }
 
-template <int DP, int NW, int PF>
+template <int DP, int NW>
 int launch_fwd_nw(const FwdParams& p, bool causal, bool has_bias, dim3 grid, hipStream_t st) {
-  // masked variants keep one register set: the bias reads need the registers
   if (causal) {
-    if (has_bias) attn_fwd_kernel<DP, NW, 1, true, true><<<grid, NW * 64, 0, st>>>(p);
-    else attn_fwd_kernel<DP, NW, PF, true, false><<<grid, NW * 64, 0, st>>>(p);
+    if (has_bias) attn_fwd_kernel<DP, NW, true, true><<<grid, NW * 64, 0, st>>>(p);
+    else attn_fwd_kernel<DP, NW, true, false><<<grid, NW * 64, 0, st>>>(p);
   } else {
-    if (has_bias) attn_fwd_kernel<DP, NW, 1, false, true><<<grid, NW * 64, 0, st>>>(p);
-    else attn_fwd_kernel<DP, NW, PF, false, false><<<grid, NW * 64, 0, st>>>(p);
+    if (has_bias) attn_fwd_kernel<DP, NW, false, true><<<grid, NW * 64, 0, st>>>(p);
+    else attn_fwd_kernel<DP, NW, false, false><<<grid, NW * 64, 0, st>>>(p);
   }
   TB_LAUNCH_CHECK("attn_fwd");
   return 0;
 }
 
-// 8-wave blocks (256 queries) share each converted K/V tile between more queries;
-// 4-wave blocks (128 queries, two blocks per CU) overlap better on their own,
-// since the two co-resident blocks run out of phase. Measured on MI355X (causal,
-// B = 1, H = 16, D = 128): 8 waves win at S = 4096 (256 blocks), 4 waves at
-// S = 16384 (1024 blocks). Head dim 256 always uses 4-wave blocks (one wave per
-// SIMD, 512 registers).
+// 8-wave blocks (256 queries, two waves per SIMD) share each K/V tile between
+// more queries and win once there are enough of them: measured on MI355X
+// (causal, D = 128) at S = 16384, B = 1, H = 16 (1024 blocks of 8 waves, 962 vs
+// 925 TFLOPS) and at S = 4096, B = 2, H = 16 (512 blocks, 632 vs 611). With at
+// most ~1.5 rounds of 8-wave blocks a causal grid is better served by 4-wave
+// blocks that pair a heavy and a light query tile (S = 4096, B = 1: 563 vs 476).
+// Head dim 256 always uses 4-wave blocks (one wave per SIMD, 512 registers).
 template <int DP>
 int launch_fwd_dp(FwdParams p, bool causal, bool has_bias, hipStream_t st, int nw_override) {
   const int64_t tiles8 = cdiv(p.Sq, 256) * p.B * p.H, tiles4 = cdiv(p.Sq, 128) * p.B * p.H;
-  // causal with at most ~4 blocks per CU: 4-wave blocks that pair a heavy and a
-  // light query tile, so every block has the same work (heaviest-first ordering
-  // only balances many rounds); otherwise as measured above
-  const bool pair = causal && tiles4 >= 2 * p.B * p.H && tiles4 <= 1024 && nw_override <= 0 &&
+  // causal with few blocks: 4-wave blocks that pair a heavy and a light query
+  // tile, so every block has the same work (heaviest-first ordering only
+  // balances many rounds); otherwise as measured above
+  const bool pair = causal && tiles4 >= 2 * p.B * p.H && tiles8 < 384 && nw_override <= 0 &&
                     getenv("TBF16_ATTN_NOPAIR") == nullptr;
-  int nw = nw_override > 0 ? nw_override : pair ? 4 : (tiles8 >= 128 && tiles8 < 1024 ? 8 : 4);
+  int nw = nw_override > 0 ? nw_override : pair ? 4 : (tiles8 >= 128 ? 8 : 4);
   if (DP > 128) nw = 4;
   const int64_t ntiles = cdiv(p.Sq, nw == 8 ? 256 : 128);
   p.pair = pair && nw == 4;
   const dim3 grid(p.B * p.H, (unsigned)(p.pair ? cdiv(ntiles, 2) : ntiles));
   if (nw == 8) {
-    if constexpr (DP <= 128) return launch_fwd_nw<DP, 8, 2>(p, causal, has_bias, grid, st);
+    if constexpr (DP <= 128) return launch_fwd_nw<DP, 8>(p, causal, has_bias, grid, st);
   }
-  return launch_fwd_nw<DP, 4, 1>(p, causal, has_bias, grid, st);
+  return launch_fwd_nw<DP, 4>(p, causal, has_bias, grid, st);
 }
 
 int check_bhsd(const char* fn, const char* name, const void* x, const int64_t* st, int64_t D) {

@@ -175,8 +175,13 @@ __device__ __forceinline__ void buf_load16_lds(BufRes r, uint32_t lds_byte, int 
   raw_buffer_load_lds(d, (lds_void*)(uintptr_t)__builtin_amdgcn_readfirstlane(lds_byte), 16, voffset,
                       __builtin_amdgcn_readfirstlane(soffset), 0, 0);
 }
-// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left at their maxima): at most N vector
+// memory loads still outstanding (loads complete in issue order)
+template <int N = 0>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N <= 15, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
 // LDS byte address of a __shared__ object
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const lds_void*)p;
