@@ -183,13 +183,13 @@ __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
 
 // ---- dK, dV --------------------------------------------------------------------
 // Block = 128 keys (32 per wave, K16 fragments in registers, the wave's V16 rows
-// in a private LDS region), loop over 64-query tiles (and over the query heads of
-// a GQA group). Q16 and dO16 tiles sit in LDS once, row-major: they are the A
-// operand of S = Q K^T and dP = dO V^T (lane = ONE key, 16 queries), and their
-// transposes for dV += P^T dO and dK += dS^T Q come from ds_read_b64_tr_b16, so P
-// and dS feed the MFMAs straight from registers. Each tile is handled as two
-// 32-query halves; without a bias a wave stays within 256 registers and two
-// blocks share a CU.
+// in a private LDS region), loop over 32-query tiles (and over the query heads of
+// a GQA group), double-buffered in LDS by direct global -> LDS loads. Q16 and
+// dO16 tiles sit in LDS once, row-major: they are the A operand of S = Q K^T and
+// dP = dO V^T (lane = ONE key, 16 queries), and their transposes for dV += P^T dO
+// and dK += dS^T Q come from ds_read_b64_tr_b16, so P and dS feed the MFMAs
+// straight from registers. Without a bias a wave stays within 256 registers and
+// two blocks share a CU.
 template <int DP, bool CAUSAL, bool HAS_BIAS>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS ? 1 : 2, HAS_BIAS ? 1 : 2))) void
 dkdv_kernel(BwdParams p) {
@@ -197,14 +197,21 @@ dkdv_kernel(BwdParams p) {
   constexpr int KS = DP / 16, DB = DP / 32, CPR = DP / 8;
   constexpr int TILE = BQ * DP * 2;   // one 32 x DP fp16 tile
   constexpr int VW = 32 * DP * 2;     // one wave's V rows
-  constexpr int CH = BQ * CPR / NTH;  // 16-byte chunks per thread per tile
   constexpr int STG = 2 * TILE;       // one stage: Q16 and dO16 tiles
-  constexpr int MAIN = 4 * VW + 2 * STG, OUT = BK * DP * 4;
-  __shared__ __align__(16) uint8_t smem[MAIN > OUT ? MAIN : OUT];
+  // stages filled by direct global -> LDS loads, 1 KB per wave instruction
+  constexpr int NBLK = STG / 1024, QBLK = TILE / 1024, BPW = NBLK / (NTH / 64);
+  static_assert(NBLK % (NTH / 64) == 0 && QBLK % BPW == 0, "stage blocks");
+  // V rows of the four waves (also the epilogue's staging, 64 keys per pass), and
+  // the two stages as separate objects: the compiler's LDS alias analysis then
+  // sees that reads of one stage never wait for the loads into the other
+  __shared__ __align__(1024) uint8_t smem[4 * VW];
+  __shared__ __align__(1024) uint8_t sst0[STG];
+  __shared__ __align__(1024) uint8_t sst1[STG];
   __shared__ __align__(16) float s_lse[2][BQ];
   __shared__ __align__(16) float s_delta[2][BQ];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, fr = lane & 31, fk = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, fr = lane & 31, fk = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // grid (heads, key blocks): dispatch runs over heads first, so every head's
   // heaviest key blocks (the most query tiles under a causal mask) go out first
   const int bk = blockIdx.x, b = bk / p.Hkv, hk = bk % p.Hkv;
@@ -240,40 +247,43 @@ dkdv_kernel(BwdParams p) {
   const int qt0 = CAUSAL ? min(k0 / BQ, nqt) : 0;
   const int total = group * (nqt - qt0);
 
-  // Query tiles of 32 rows in two LDS stages (tile it in stage it % 2). The loads
-  // of tile it + 1 (thread t: 16-byte chunks t + 256 i of the Q16 and dO16 tiles,
-  // threads < 32 also the rows' lse and delta) are issued when tile it starts
-  // and stored into the other stage after tile it's S / dP products, so they
-  // have those MFMAs to land; one barrier per tile publishes the stage and
-  // retires the reads of the one it overwrote.
-  uint4 rq[CH], rd[CH];
-  float rl = INFINITY, rdl = 0.f;
-  auto gload = [&](int it) {
-    const int h = hk * group + it / (nqt - qt0);
-    const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
-    const int bh = b * p.H + h;
-    const int64_t base = ((int64_t)bh * p.Sqp + q0) * DP;
+  // Query tiles of 32 rows in two LDS stages (tile it in stage it % 2). When tile
+  // it starts, threads < 32 load tile it + 1's lse and delta into registers (for
+  // s_lse / s_delta after tile it's S / dP products) and then every wave issues
+  // its share of tile it + 1's Q16 and dO16 rows as direct global -> LDS loads
+  // (lane j of an instruction lands at byte 16 j of its 1 KB block, so the row
+  // swizzle is applied on the source side); the barrier that ends tile it waits
+  // for them.
+  int voff[BPW];
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
-      rq[i] = ldg16(p.q16 + base + row * DP + ch * 8);
-      rd[i] = ldg16(p.do16 + base + row * DP + ch * 8);
-    }
+  for (int i = 0; i < BPW; ++i) {
+    const int byte = ((wave * BPW + i) % QBLK) * 1024 + 16 * lane, row = byte / (2 * DP), phys = (byte % (2 * DP)) >> 4;
+    const int lch = (swz_row<DP>(row, phys) - row * 2 * DP) >> 4;  // the XOR swizzle is its own inverse
+    voff[i] = (row * DP + lch * 8) * 2;
+  }
+  float rl = INFINITY, rdl = 0.f;
+  auto tile_src = [&](int it, int& bh, int& q0) {
+    const int h = hk * group + it / (nqt - qt0);
+    q0 = (qt0 + it % (nqt - qt0)) * BQ;
+    bh = b * p.H + h;
+  };
+  auto gload = [&](int it, uint8_t* stage) {
+    int bh, q0;
+    tile_src(it, bh, q0);
     if (tid < BQ) {
       const int qi = q0 + tid;
       rl = qi < p.Sq ? p.lse[(int64_t)bh * p.Sq + qi] : INFINITY;
       rdl = qi < p.Sq ? p.delta[(int64_t)bh * p.Sq + qi] : 0.f;
     }
+    const int64_t row0 = ((int64_t)bh * p.Sqp + q0) * DP;
+    // blocks [0, QBLK) of a stage hold Q16 rows, the rest dO16 rows; a wave's
+    // BPW blocks all lie on one side (QBLK is a multiple of BPW)
+    const BufRes res = make_res((wave * BPW < QBLK ? p.q16 : p.do16) + row0, TILE);
+    const uint32_t base = lds_addr(stage);
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) buf_load16_lds(res, base + (wave * BPW + i) * 1024, voff[i], 0);
   };
   auto lstore = [&](int stg) {
-    uint8_t* sQ = smem + 4 * VW + stg * STG;
-    uint8_t* sD = sQ + TILE;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
-      *reinterpret_cast<uint4*>(sQ + swz_row<DP>(row, ch)) = rq[i];
-      *reinterpret_cast<uint4*>(sD + swz_row<DP>(row, ch)) = rd[i];
-    }
     if (tid < BQ) {
       s_lse[stg][tid] = rl;
       s_delta[stg][tid] = rdl;
@@ -281,17 +291,16 @@ dkdv_kernel(BwdParams p) {
   };
 
   if (total > 0) {
-    gload(0);
+    gload(0, sst0);
     lstore(0);
   }
+  wait_vmem();
   __syncthreads();
-  for (int it = 0; it < total; ++it) {
-    const int stg = it & 1;
+  auto tile = [&](int it, const uint8_t* sQ, uint8_t* snext, int stg) {
     const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
-    const uint8_t* sQ = smem + 4 * VW + stg * STG;
     const uint8_t* sD = sQ + TILE;
     const bool more = it + 1 < total;
-    if (more) gload(it + 1);
+    if (more) gload(it + 1, snext);
 
     const bool edge = q0 + BQ > p.Sq || k0 + BK > p.Sk || (CAUSAL && k0 + wave * 32 + 31 >= q0);
     // with a bias the logits are scaled and biased first, as in the forward pass
@@ -309,7 +318,15 @@ dkdv_kernel(BwdParams p) {
       sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kf[s], sacc, 0, 0, 0);
       pacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, vb, pacc, 0, 0, 0);
     }
-    // the next tile's stage: its reads retired at the previous barrier
+    // fragment reads one k step ahead of the MFMAs that use them
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      if (s + 1 < KS) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the next tile's lse and delta: their slots' reads retired at the previous barrier
     if (more) lstore(stg ^ 1);
     if constexpr (HAS_BIAS) {
 #pragma unroll
@@ -374,35 +391,45 @@ dkdv_kernel(BwdParams p) {
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     __builtin_amdgcn_sched_barrier(0);
+    wait_vmem();
     __syncthreads();
+  };
+  for (int it = 0; it < total; it += 2) {
+    tile(it, sst0, sst1, 0);
+    if (it + 1 < total) tile(it + 1, sst1, sst0, 1);
   }
 
   // ---- epilogue: lane = key row (fr), d = db*32 + 8*(r/4) + 4*fk + r%4 ----
   // dV / dK accumulators are C[key][d] with key = MFMA row: lane holds col d = fr and
-  // rows key = 8*(r/4) + 4*fk + r%4. Transpose through LDS for 16-byte stores.
+  // rows key = 8*(r/4) + 4*fk + r%4. Transpose through LDS for 16-byte stores, 64
+  // keys (two waves' rows) per pass.
   __syncthreads();
-  float* sOut = reinterpret_cast<float*>(smem);  // 128 keys x DP floats per pass
+  float* sOut = reinterpret_cast<float*>(smem);  // 64 keys x DP floats
   const float sk_out = ldexp1(-a - G) * p.scale, sv_out = ldexp1(-ev - G);
   bool bad = false;
-  for (int pass = 0; pass < 2; ++pass) {
-    floatx16* acc = pass == 0 ? dv : dk;
-    const float so = pass == 0 ? sv_out : sk_out;
-    const float chk = pass == 0 ? 1.f : p.scale;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+  for (int pass = 0; pass < 4; ++pass) {
+    const int kind = pass >> 1, half = pass & 1;
+    floatx16* acc = kind == 0 ? dv : dk;
+    const float so = kind == 0 ? sv_out : sk_out;
+    const float chk = kind == 0 ? 1.f : p.scale;
+    if ((wave >> 1) == half) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kl = wave * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
-        const int d = db * 32 + fr;
-        const float x = acc[db][r];
-        if (k0 + kl < p.Sk && d < p.D) bad |= bad16(x * chk);
-        sOut[kl * DP + d] = x * so;
-      }
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kl = (wave & 1) * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
+          const int d = db * 32 + fr;
+          const float x = acc[db][r];
+          if (k0 + half * 64 + kl < p.Sk && d < p.D) bad |= bad16(x * chk);
+          sOut[kl * DP + d] = x * so;
+        }
+    }
     __syncthreads();
-    uint16_t* out = pass == 0 ? p.dv : p.dk;
-    for (int i = tid; i < BK * (DP / 8); i += NTH) {
+    uint16_t* out = kind == 0 ? p.dv : p.dk;
+    for (int i = tid; i < 64 * (DP / 8); i += NTH) {
       const int kl = i / (DP / 8), d = (i % (DP / 8)) * 8;
-      const int kk = k0 + kl;
+      const int kk = k0 + half * 64 + kl;
       if (kk < p.Sk && d < p.D) {
         const float* src = sOut + kl * DP + d;
         stg16(out + ((int64_t)bk * p.Sk + kk) * p.D + d,
@@ -417,21 +444,28 @@ dkdv_kernel(BwdParams p) {
 
 // ---- dQ --------------------------------------------------------------------------
 // Two blocks per CU (two waves per SIMD, without a bias): a wave's dO rows live in
-// a private LDS region instead of registers, and each 64-key tile is processed as
-// two 32-key halves, which keeps a wave within 256 registers.
+// a private LDS region instead of registers, and K/V arrive in 32-key tiles
+// (double-buffered, direct global -> LDS loads), which keeps a wave within 256
+// registers.
 template <int DP, bool CAUSAL, bool HAS_BIAS>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS ? 1 : 2, HAS_BIAS ? 1 : 2))) void
 dq_kernel(BwdParams p) {
-  constexpr int BQ = 128, BKV = 64;
+  constexpr int BQ = 128, BKV = 32;
   constexpr int KS = DP / 16, DB = DP / 32;
-  constexpr int TILE = BKV * DP * 2;
-  constexpr int CPR = DP / 8, CH = BKV * CPR / NTH;  // 16-byte chunks per thread per tile
+  constexpr int TILE = BKV * DP * 2;  // 32 key rows of K16 (or V16)
+  constexpr int STG = 2 * TILE;       // one stage: K16 rows, then V16 rows
+  constexpr int NBLK = STG / 1024, KBLK = TILE / 1024, BPW = NBLK / (NTH / 64);
+  static_assert(NBLK % (NTH / 64) == 0 && KBLK % BPW == 0, "stage blocks");
   constexpr int DOW = 32 * DP * 2;  // one wave's dO rows
-  __shared__ __align__(16) uint8_t smem[2 * TILE + 4 * DOW];  // K, V, dO (per wave)
-  uint8_t* sK = smem;
-  uint8_t* sV = smem + TILE;
+  // per-wave dO rows and two K/V stages as separate objects (the compiler's LDS
+  // alias analysis then sees that reads of one stage never wait for the direct
+  // loads into the other)
+  __shared__ __align__(1024) uint8_t smem[4 * DOW];
+  __shared__ __align__(1024) uint8_t sst0[STG];
+  __shared__ __align__(1024) uint8_t sst1[STG];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, fr = lane & 31, fk = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, fr = lane & 31, fk = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // grid (heads, query blocks), heaviest query blocks of every head first
   const int bh = blockIdx.x, b = bh / p.H, h = bh % p.H, hk = h / (p.H / p.Hkv);
   const int qt = CAUSAL ? (int)(gridDim.y - 1 - blockIdx.y) : (int)blockIdx.y;
@@ -442,7 +476,7 @@ dq_kernel(BwdParams p) {
 
   const int qrow = q0 + wave * 32 + fr;
   half8 qf[KS];
-  uint8_t* sDo = smem + 2 * TILE + wave * DOW;  // written and read by this wave only
+  uint8_t* sDo = smem + wave * DOW;  // written and read by this wave only
   {
     // padded copies: qrow < Sqp and d < DP always lie inside
     const uint16_t* qr = p.q16 + ((int64_t)bh * p.Sqp + qrow) * DP;
@@ -462,49 +496,45 @@ dq_kernel(BwdParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[i][r] = 0.f;
 
-  const int nkb_all = (p.Sk + BKV - 1) / BKV;
-  const int nkb = CAUSAL ? min(nkb_all, (min(q0 + BQ, p.Sq) + BKV - 1) / BKV) : nkb_all;
-  const uint16_t* kbase = p.k16 + (int64_t)(b * p.Hkv + hk) * p.Skp * DP;
-  const uint16_t* vbase = p.v16 + (int64_t)(b * p.Hkv + hk) * p.Skp * DP;
-  // tile staging: thread t moves 16-byte chunks t + 256 i (row c / CPR, chunk
-  // c % CPR) of the K16 and V16 tiles (the padded copies: zeros past Sk and D)
-  uint4 rk[CH], rv[CH];
-  auto gload = [&](int kb) {
+  // 32-key tiles in two stages (tile t in stage t % 2), the padded copies (zeros
+  // past Sk and D) copied global -> LDS directly: lane j of a wave instruction
+  // lands at byte 16 j of its 1 KB block, so the row swizzle is applied on the
+  // source side. Tile t + 1's loads go out when tile t starts; the barrier that
+  // ends tile t waits for them.
+  const int nk = CAUSAL ? min(p.Sk, min(q0 + BQ, p.Sq)) : p.Sk;
+  const int nt = (nk + BKV - 1) / BKV;
+  int voff[BPW];
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + i * NTH, row = kb * BKV + c / CPR, ch = c % CPR;
-      rk[i] = ldg16(kbase + row * DP + ch * 8);
-      rv[i] = ldg16(vbase + row * DP + ch * 8);
-    }
+  for (int i = 0; i < BPW; ++i) {
+    const int byte = ((wave * BPW + i) % KBLK) * 1024 + 16 * lane, row = byte / (2 * DP), phys = (byte % (2 * DP)) >> 4;
+    const int lch = (swz_row<DP>(row, phys) - row * 2 * DP) >> 4;  // the XOR swizzle is its own inverse
+    voff[i] = (row * DP + lch * 8) * 2;
+  }
+  const uint16_t* kvsrc = (wave * BPW < KBLK ? p.k16 : p.v16) + (int64_t)(b * p.Hkv + hk) * p.Skp * DP;
+  auto dload = [&](uint8_t* stage, int t) {
+    const BufRes res = make_res(kvsrc + (int64_t)t * BKV * DP, TILE);
+    const uint32_t base = lds_addr(stage);
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) buf_load16_lds(res, base + (wave * BPW + i) * 1024, voff[i], 0);
   };
   const uint16_t* brow = nullptr;
   if constexpr (HAS_BIAS)
     brow = p.bias + (int64_t)b * p.bias_sb + (int64_t)h * p.bias_sh + (int64_t)min(qrow, p.Sq - 1) * p.bias_sq;
 
-  if (nkb > 0) gload(0);
-  for (int kb = 0; kb < nkb; ++kb) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + i * NTH, row = c / CPR, ch = c % CPR;
-      *reinterpret_cast<uint4*>(sK + swz_row<DP>(row, ch)) = rk[i];
-      *reinterpret_cast<uint4*>(sV + swz_row<DP>(row, ch)) = rv[i];
-    }
-    __syncthreads();
-    if (kb + 1 < nkb) gload(kb + 1);
-
-    // per 32-key half: S^T and dP^T (lane = one query, 16 keys), then dS and its
-    // two 16-key steps of dQ^T += K^T dS^T
-    const float cs = HAS_BIAS ? 1.f : p.scale_log2;  // with a bias: scaled and biased first
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
+  // one 32-key tile: S^T and dP^T (lane = one query, 16 keys), then dS and its
+  // two 16-key steps of dQ^T += K^T dS^T
+  const float cs = HAS_BIAS ? 1.f : p.scale_log2;  // with a bias: scaled and biased first
+  auto tile = [&](int t, const uint8_t* sK, uint8_t* snext) {
+    if (t + 1 < nt) dload(snext, t + 1);
+    const uint8_t* sV = sK + TILE;
+    {
       floatx16 sacc, pacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const half8 ka = *reinterpret_cast<const half8*>(sK + swz_row<DP>(kh * 32 + fr, 2 * s + fk));
-        const half8 va = *reinterpret_cast<const half8*>(sV + swz_row<DP>(kh * 32 + fr, 2 * s + fk));
+        const half8 ka = *reinterpret_cast<const half8*>(sK + swz_row<DP>(fr, 2 * s + fk));
+        const half8 va = *reinterpret_cast<const half8*>(sV + swz_row<DP>(fr, 2 * s + fk));
         const half8 dfs = *reinterpret_cast<const half8*>(sDo + swz_row<DP>(fr, 2 * s + fk));
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[s], sacc, 0, 0, 0);
         pacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, dfs, pacc, 0, 0, 0);
@@ -518,7 +548,7 @@ dq_kernel(BwdParams p) {
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
       __builtin_amdgcn_sched_barrier(0);
-      const int kb0 = kb * BKV + kh * 32;
+      const int kb0 = t * BKV;
       if constexpr (HAS_BIAS) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -526,8 +556,8 @@ dq_kernel(BwdParams p) {
           sacc[r] = sacc[r] * p.scale_log2 + (kk < p.Sk ? (float)__builtin_bit_cast(_Float16, brow[kk]) * kLog2e : 0.f);
         }
       }
-      // masking only where the half crosses the diagonal or an end
-      if (kb0 + 32 > p.Sk || q0 + BQ > p.Sq || (CAUSAL && kb0 + 31 > q0 + wave * 32)) {
+      // masking only where the tile crosses the diagonal or an end
+      if (kb0 + BKV > p.Sk || q0 + BQ > p.Sq || (CAUSAL && kb0 + BKV - 1 > q0 + wave * 32)) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kk = kb0 + 8 * (r >> 2) + 4 * fk + (r & 3);
@@ -543,11 +573,11 @@ dq_kernel(BwdParams p) {
       }
 #pragma unroll
       for (int kq = 0; kq < 2; ++kq) {
-        const int ks = 2 * kh + kq, o = 4 * kq;
+        const int o = 4 * kq;
         const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[o], ds[o + 1], ds[o + 2], ds[o + 3]));
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const half8 kbf = tr_frag<DP>(sK, 16 * ks, db * 32, lane);  // K^T fragment
+          const half8 kbf = tr_frag<DP>(sK, 16 * kq, db * 32, lane);  // K^T fragment
           dq[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kbf, sa, dq[db], 0, 0, 0);
         }
       }
@@ -561,6 +591,15 @@ dq_kernel(BwdParams p) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
+    wait_vmem();
+    __syncthreads();
+  };
+  if (nt > 0) dload(sst0, 0);
+  wait_vmem();
+  __syncthreads();
+  for (int t = 0; t < nt; t += 2) {
+    tile(t, sst0, sst1);
+    if (t + 1 < nt) tile(t + 1, sst1, sst0);
   }
 
   // dQ^T accumulators: lane col = query (fr), rows d = db*32 + 8*(r/4) + 4*fk + r%4
