@@ -371,41 +371,45 @@ attn_fwd_kernel(FwdParams p) {
       };
       half8 vf[VPRE ? 4 : 1][DB];
       if constexpr (VPRE) {
-        half8 kf[2][KS];
+        // One read queue: the K fragments in MFMA order, the two halves' chains
+        // alternating (consecutive MFMAs never depend on each other: a dependent
+        // MFMA waits for its predecessor's result), then the V^T fragments of PV
+        // steps 0 and 1; reads run LA MFMAs ahead, two per MFMA at first.
+        constexpr int LA = 4, NK = 2 * KS, NQ = NK + 2 * DB, EXTRA = NQ - LA - NK;
+        static_assert(EXTRA >= 0 && EXTRA <= NK, "read queue");
+        half8 fq[NQ];
   #pragma unroll
-        for (int s = 0; s < KS; ++s) kf[0][s] = kread(0, s);
+        for (int j = 0; j < NQ; ++j) {
+          if (j < NK) fq[j] = kread(j & 1, j >> 1);
+          else fq[j] = vread((j - NK) / DB, (j - NK) % DB);
+        }
         deferred();
   #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0][s], qf[s], sacc[0], 0, 0, 0);
-          kf[1][s] = kread(1, s);
-        }
-  #pragma unroll
-        for (int s = 0; s < KS; ++s) sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[1][s], qf[s], sacc[1], 0, 0, 0);
+        for (int j = 0; j < NK; ++j)
+          sacc[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fq[j], qf[j >> 1], sacc[j & 1], 0, 0, 0);
   #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
   #pragma unroll
-          for (int db = 0; db < DB; ++db) vf[ks][db] = vread(ks, db);
-        constexpr int VR = (2 * DB + KS - 1) / KS;  // V^T reads per MFMA of the second half
-        __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);
+          for (int db = 0; db < DB; ++db) vf[ks][db] = fq[NK + ks * DB + db];
+        __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, DB, 0);  // the previous tile's deferred step
   #pragma unroll
-        for (int i = 0; i < KS; ++i) {
+        for (int i = 0; i < EXTRA; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
   #pragma unroll
-        for (int i = 0; i < KS; ++i) {
+        for (int i = EXTRA; i < NK; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if (i * VR < 2 * DB) __builtin_amdgcn_sched_group_barrier(0x100, VR, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
       } else {
         deferred();
   #pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
+        for (int s = 0; s < KS; ++s)
   #pragma unroll
-          for (int s = 0; s < KS; ++s) sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kread(kh, s), qf[s], sacc[kh], 0, 0, 0);
+          for (int kh = 0; kh < 2; ++kh) sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kread(kh, s), qf[s], sacc[kh], 0, 0, 0);
       }
       const int key0 = kb * BKV;
       const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0 + wave * 32);
