@@ -140,7 +140,8 @@ int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64
  * *overflow is set to 1 (device int, caller zeroes it) when any gradient in the
  * scaled fp16 domain would overflow fp16 (|x| >= 65520) or is not finite, which
  * is the reference's retry condition (tbf16/autograd.py:177-189). exps_out int32
- * [2] = {e, G}. Inputs are the forward's q, k, v, o16, lse and exps.
+ * [2] = {e, G}. Inputs are the forward's q, k, v, o16, lse and exps; same shape
+ * rules as the forward (D % 8 == 0, D <= 256).
  * Replaces torch's _scaled_dot_product_efficient_attention_backward call and the
  * surrounding scaling (tbf16/autograd.py:166-193). */
 size_t tbf16_attn_bwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);

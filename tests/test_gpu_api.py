@@ -258,7 +258,9 @@ def _ref_sdpa(q, k, v, causal, mask=None):
     ("GQA 16/4 causal", 16, 4, 1024, 128, True, 1.0, 1.0, 1.0),
     ("dO x1e-10", 8, 8, 1024, 64, True, 1.0, 1e-10, 1.0),
     ("dO x1e6, v x1e4", 8, 8, 1024, 64, True, 1.0, 1e6, 1e4),
-    ("peaky q,k x8", 8, 8, 1024, 64, True, 8.0, 1.0, 1.0)])
+    ("peaky q,k x8", 8, 8, 1024, 64, True, 8.0, 1.0, 1.0),
+    ("D=256 causal GQA 8/4", 8, 4, 640, 256, True, 1.0, 1.0, 1.0),
+    ("D=192 (padded to 256)", 4, 4, 520, 192, False, 1.0, 1.0, 1.0)])
 def test_autograd_sdpa(dev, name, Hq, Hkv, S, D, causal, qs, gs, vs):
     q = (randn(1, Hq, S, D, seed=50) * qs).bfloat16().to(dev)
     k = (randn(1, Hkv, S, D, seed=51) * qs).bfloat16().to(dev)

@@ -161,9 +161,10 @@ __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
   const float sdo = ldexp1(ev_of(p, b, h) + G);
   const int row = blockIdx.x * 16 + (threadIdx.x >> 4), l16 = threadIdx.x & 15;
   float acc = 0.f;
-  // dO16 row (zeros past Sq and past D), 8 columns per lane (DP <= 128)
+  // dO16 row (zeros past Sq and past D), 8 columns per lane
   uint16_t* wrow = p.do16 + ((int64_t)bh * p.Sqp + row) * p.DPc;
-  if (row < p.Sqp && l16 * 8 < p.DPc && (row >= p.Sq || l16 * 8 >= p.D)) stg16(wrow + l16 * 8, make_uint4(0, 0, 0, 0));
+  for (int c = l16 * 8; c < p.DPc; c += 128)
+    if (row < p.Sqp && (row >= p.Sq || c >= p.D)) stg16(wrow + c, make_uint4(0, 0, 0, 0));
   if (row < p.Sq) {
     const uint16_t* dr = p.dout + (int64_t)b * p.d_sb + (int64_t)h * p.d_sh + (int64_t)row * p.d_ss;
     const uint16_t* orow = p.o16 + ((int64_t)bh * p.Sq + row) * p.D;
@@ -190,9 +191,13 @@ __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
 // and dK += dS^T Q come from ds_read_b64_tr_b16, so P and dS feed the MFMAs
 // straight from registers. Without a bias a wave stays within 256 registers and
 // two blocks share a CU.
-template <int DP, bool CAUSAL, bool HAS_BIAS>
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS ? 1 : 2, HAS_BIAS ? 1 : 2))) void
+// PART 0 accumulates dK and dV together; for DP = 256 (whose two accumulator
+// sets and K fragments exceed a wave's 512 registers) PART 1 accumulates dV and
+// PART 2 dK, in two launches that each recompute S.
+template <int DP, bool CAUSAL, bool HAS_BIAS, int PART>
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS || DP > 128 ? 1 : 2, HAS_BIAS || DP > 128 ? 1 : 2))) void
 dkdv_kernel(BwdParams p) {
+  constexpr bool WANT_DV = PART != 2, WANT_DK = PART != 1;
   constexpr int BQ = 32, BK = 128;
   constexpr int KS = DP / 16, DB = DP / 32, CPR = DP / 8;
   constexpr int TILE = BQ * DP * 2;   // one 32 x DP fp16 tile
@@ -236,11 +241,15 @@ dkdv_kernel(BwdParams p) {
       *reinterpret_cast<uint4*>(sVw + swz_row<DP>(fr, 2 * s + fk)) = ldg16(vr + d);
     }
   }
-  floatx16 dk[DB], dv[DB];
+  floatx16 dk[WANT_DK ? DB : 1], dv[WANT_DV ? DB : 1];
 #pragma unroll
-  for (int i = 0; i < DB; ++i)
+  for (int i = 0; i < (WANT_DK ? DB : 1); ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dk[i][r] = dv[i][r] = 0.f;
+    for (int r = 0; r < 16; ++r) dk[i][r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < (WANT_DV ? DB : 1); ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
 
   const int group = p.H / p.Hkv;
   const int nqt = (p.Sq + BQ - 1) / BQ;
@@ -313,17 +322,20 @@ dkdv_kernel(BwdParams p) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const half8 qa = *reinterpret_cast<const half8*>(sQ + swz_row<DP>(fr, 2 * s + fk));
-      const half8 da = *reinterpret_cast<const half8*>(sD + swz_row<DP>(fr, 2 * s + fk));
-      const half8 vb = *reinterpret_cast<const half8*>(sVw + swz_row<DP>(fr, 2 * s + fk));
       sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kf[s], sacc, 0, 0, 0);
-      pacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, vb, pacc, 0, 0, 0);
+      if constexpr (WANT_DK) {  // dP is needed only for dS
+        const half8 da = *reinterpret_cast<const half8*>(sD + swz_row<DP>(fr, 2 * s + fk));
+        const half8 vb = *reinterpret_cast<const half8*>(sVw + swz_row<DP>(fr, 2 * s + fk));
+        pacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, vb, pacc, 0, 0, 0);
+      }
     }
     // fragment reads one k step ahead of the MFMAs that use them
-    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    constexpr int RPS = WANT_DK ? 3 : 1, MPS = WANT_DK ? 2 : 1;  // reads, MFMAs per k step
+    __builtin_amdgcn_sched_group_barrier(0x100, RPS, 0);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      if (s + 1 < KS) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, MPS, 0);
+      if (s + 1 < KS) __builtin_amdgcn_sched_group_barrier(0x100, RPS, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     // the next tile's lse and delta: their slots' reads retired at the previous barrier
@@ -361,7 +373,7 @@ dkdv_kernel(BwdParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[4 * i + j], cs, -lse4[j]));
-        dsv[j] = pv[j] * (pacc[4 * i + j] - del4[j]);
+        dsv[j] = WANT_DK ? pv[j] * (pacc[4 * i + j] - del4[j]) : 0.f;
       }
       pp[2 * i] = pack_f16(pv[0], pv[1]);
       pp[2 * i + 1] = pack_f16(pv[2], pv[3]);
@@ -376,20 +388,25 @@ dkdv_kernel(BwdParams p) {
       const half8 sa = __builtin_bit_cast(half8, make_uint4(ds[o], ds[o + 1], ds[o + 2], ds[o + 3]));
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const half8 dob = tr_frag<DP>(sD, r0, db * 32, lane);
-        const half8 qbf = tr_frag<DP>(sQ, r0, db * 32, lane);
-        dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, dob, dv[db], 0, 0, 0);
-        dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, qbf, dk[db], 0, 0, 0);
+        if constexpr (WANT_DV) {
+          const half8 dob = tr_frag<DP>(sD, r0, db * 32, lane);
+          dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, dob, dv[db], 0, 0, 0);
+        }
+        if constexpr (WANT_DK) {
+          const half8 qbf = tr_frag<DP>(sQ, r0, db * 32, lane);
+          dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa, qbf, dk[db], 0, 0, 0);
+        }
       }
     }
     // transposed reads one (kq, db) step ahead of their MFMAs
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    constexpr int TRS = PART == 0 ? 4 : 2, TMS = PART == 0 ? 2 : 1;
+    __builtin_amdgcn_sched_group_barrier(0x100, TRS, 0);
 #pragma unroll
     for (int s = 0; s + 1 < 2 * DB; ++s) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, TRS, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, TMS, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, TMS, 0);
     __builtin_amdgcn_sched_barrier(0);
     wait_vmem();
     __syncthreads();
@@ -410,6 +427,7 @@ dkdv_kernel(BwdParams p) {
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int kind = pass >> 1, half = pass & 1;
+    if ((kind == 0 && !WANT_DV) || (kind == 1 && !WANT_DK)) continue;
     floatx16* acc = kind == 0 ? dv : dk;
     const float so = kind == 0 ? sv_out : sk_out;
     const float chk = kind == 0 ? 1.f : p.scale;
@@ -448,7 +466,7 @@ dkdv_kernel(BwdParams p) {
 // (double-buffered, direct global -> LDS loads), which keeps a wave within 256
 // registers.
 template <int DP, bool CAUSAL, bool HAS_BIAS>
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS ? 1 : 2, HAS_BIAS ? 1 : 2))) void
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS || DP > 128 ? 1 : 2, HAS_BIAS || DP > 128 ? 1 : 2))) void
 dq_kernel(BwdParams p) {
   constexpr int BQ = 128, BKV = 32;
   constexpr int KS = DP / 16, DB = DP / 32;
@@ -632,13 +650,13 @@ struct BwdWs {
 };
 
 // partial dO maxima | delta (B, H, Sq) fp32 | q16, dO16 (B, H, Sqp, DP) | k16, v16
-// (B, Hkv, Skp, DP), rows padded to a multiple of 128, DP = 64 or 128
+// (B, Hkv, Skp, DP), rows padded to a multiple of 128, DP = 64, 128 or 256
 BwdWs bwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
   BwdWs w;
   w.nch = head_amax_chunks(B * H, Sq);
   w.Sqp = cdiv(Sq, 128) * 128;
   w.Skp = cdiv(Sk, 128) * 128;
-  w.DP = D <= 64 ? 64 : 128;
+  w.DP = D <= 64 ? 64 : D <= 128 ? 128 : 256;
   w.off_delta = align_up((size_t)(B * H * w.nch) * 4, 256);
   w.off_q16 = w.off_delta + align_up((size_t)(B * H * Sq) * 4, 256);
   const size_t qb = align_up((size_t)(B * H * w.Sqp * w.DP) * 2, 256), kb = align_up((size_t)(B * Hkv * w.Skp * w.DP) * 2, 256);
@@ -653,10 +671,17 @@ template <int DP>
 int launch_bwd_dp(const BwdParams& p, bool causal, bool has_bias, hipStream_t st) {
   dim3 g_kv((unsigned)(p.B * p.Hkv), (unsigned)cdiv(p.Sk, 128));
   dim3 g_q((unsigned)(p.B * p.H), (unsigned)cdiv(p.Sq, 128));
-#define LAUNCH(C, HB)                                  \
-  dkdv_kernel<DP, C, HB><<<g_kv, NTH, 0, st>>>(p);     \
-  TB_LAUNCH_CHECK("attn_bwd/dkdv");                    \
-  dq_kernel<DP, C, HB><<<g_q, NTH, 0, st>>>(p);        \
+#define LAUNCH(C, HB)                                        \
+  if constexpr (DP > 128) {                                  \
+    dkdv_kernel<DP, C, HB, 1><<<g_kv, NTH, 0, st>>>(p);      \
+    TB_LAUNCH_CHECK("attn_bwd/dv");                          \
+    dkdv_kernel<DP, C, HB, 2><<<g_kv, NTH, 0, st>>>(p);      \
+    TB_LAUNCH_CHECK("attn_bwd/dk");                          \
+  } else {                                                   \
+    dkdv_kernel<DP, C, HB, 0><<<g_kv, NTH, 0, st>>>(p);      \
+    TB_LAUNCH_CHECK("attn_bwd/dkdv");                        \
+  }                                                          \
+  dq_kernel<DP, C, HB><<<g_q, NTH, 0, st>>>(p);              \
   TB_LAUNCH_CHECK("attn_bwd/dq");
   if (causal) {
     if (has_bias) { LAUNCH(true, true) } else { LAUNCH(true, false) }
@@ -681,7 +706,7 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
                               void* dv, int32_t* exps_out, int32_t* overflow, void* ws, int64_t ws_bytes,
                               void* stream) {
   TB_CHECK(B >= 0 && H > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0 && H % Hkv == 0, "attn_bwd: bad shape");
-  TB_CHECK(D > 0 && D % 8 == 0 && D <= 128, "attn_bwd: head dim must be a multiple of 8 up to 128");
+  TB_CHECK(D > 0 && D % 8 == 0 && D <= 256, "attn_bwd: head dim must be a multiple of 8 up to 256");
   TB_CHECK(q && k && v && o16 && lse && dout && exps_fwd && dq && dk && dv && exps_out && overflow,
            "attn_bwd: null argument");
   TB_CHECK(q_strides && k_strides && v_strides && do_strides, "attn_bwd: strides missing");
@@ -728,5 +753,6 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
   delta_kernel<<<dim3((unsigned)cdiv(w.Sqp, 16), (unsigned)(B * H)), NTH, 0, st>>>(p);
   TB_LAUNCH_CHECK("attn_bwd/delta");
   if (D <= 64) return launch_bwd_dp<64>(p, causal != 0, bias != nullptr, st);
-  return launch_bwd_dp<128>(p, causal != 0, bias != nullptr, st);
+  if (D <= 128) return launch_bwd_dp<128>(p, causal != 0, bias != nullptr, st);
+  return launch_bwd_dp<256>(p, causal != 0, bias != nullptr, st);
 }
