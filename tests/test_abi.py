@@ -62,7 +62,7 @@ def test_host_validation_rejects_before_launch():
                             16, 0, None) == -1
     assert "workspace" in _err()
     # backward head dim limit
-    assert L.tbf16_attn_bwd(16, 16, 16, 16, 16, 16, 16, 1, 2, 2, 8, 8, 256, st, st, st, st, None, None, 1.0, 0, 5,
+    assert L.tbf16_attn_bwd(16, 16, 16, 16, 16, 16, 16, 1, 2, 2, 8, 8, 264, st, st, st, st, None, None, 1.0, 0, 5,
                             16, 16, 16, 16, 16, 16, 1 << 20, None) == -1
 
 
