@@ -124,14 +124,20 @@ int tbf16_head_scale_cast(const void* x, int in_dtype, int64_t B, int64_t H, int
  * Outputs: o bf16 (B, H, Sq, D) contiguous; optional lse fp32 (B, H, Sq) in log2
  * units of (logit * scale * log2(e)); optional o16 fp16 (B, H, Sq, D) = O / l
  * (saved for the backward); optional exps int32 [2 + B*Hkv] = {a, 0, ev...}.
+ * dropout_p in [0, 1): attention weights dropped by a counter-based hash of
+ * (seed, b*H + h, query, key) (MurmurHash3 fmix32 finalizer, see the device
+ * helpers), kept ones scaled by 1 / (1 - p); l and lse use the undropped weights,
+ * so tbf16_attn_bwd with the same seed and p regenerates the mask. The reference
+ * passes dropout_p to torch's kernel, whose Philox stream differs: masks are not
+ * comparable bit for bit.
  * Replaces prepare_qkv + torch's fp16 memory-efficient SDPA + head_scale
  * (tbf16/attention.py:285-294) and _eff_fwd (tbf16/autograd.py:155-164). */
 size_t tbf16_attn_fwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);
 int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t Hkv, int64_t Sq,
                    int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
                    const int64_t* v_strides, const void* bias, const int64_t* bias_strides, float scale, int causal,
-                   int v_exp, void* o, float* lse, void* o16, int32_t* exps, void* ws, int64_t ws_bytes,
-                   void* stream);
+                   int v_exp, float dropout_p, uint64_t seed, void* o, float* lse, void* o16, int32_t* exps,
+                   void* ws, int64_t ws_bytes, void* stream);
 
 /* Scaled attention backward for one value of the dO target exponent t_do.
  * e = max(frexp(amax dout[b,h]) + ev_q[b,h]), G = t_do - e, dO16 = fp16(dout *
@@ -141,7 +147,9 @@ int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64
  * scaled fp16 domain would overflow fp16 (|x| >= 65520) or is not finite, which
  * is the reference's retry condition (tbf16/autograd.py:177-189). exps_out int32
  * [2] = {e, G}. Inputs are the forward's q, k, v, o16, lse and exps; same shape
- * rules as the forward (D % 8 == 0, D <= 256).
+ * rules as the forward (D % 8 == 0, D <= 256); dropout_p and seed as given to
+ * the forward (its mask is regenerated: dV from P o Z, dS = P o (Z o dP - delta)
+ * with Z = keep / (1 - p)).
  * Replaces torch's _scaled_dot_product_efficient_attention_backward call and the
  * surrounding scaling (tbf16/autograd.py:166-193). */
 size_t tbf16_attn_bwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);
@@ -149,8 +157,9 @@ int tbf16_attn_bwd(const void* q, const void* k, const void* v, const void* o16,
                    const void* dout, const int32_t* exps_fwd, int64_t B, int64_t H, int64_t Hkv, int64_t Sq,
                    int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
                    const int64_t* v_strides, const int64_t* do_strides, const void* bias,
-                   const int64_t* bias_strides, float scale, int causal, int t_do, void* dq, void* dk, void* dv,
-                   int32_t* exps_out, int32_t* overflow, void* ws, int64_t ws_bytes, void* stream);
+                   const int64_t* bias_strides, float scale, int causal, int t_do, float dropout_p, uint64_t seed,
+                   void* dq, void* dk, void* dv, int32_t* exps_out, int32_t* overflow, void* ws, int64_t ws_bytes,
+                   void* stream);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,11 @@ How each function is pinned (checked by tests/test_oracle.py):
                               logits copy a V row; fp64 autograd for gradients.
   attn_bwd_exponents / retry  closed form of autograd.py:175-189 with an injected
                               overflowing backward.
+  fmix32 / dropout_keep       this build's own dropout mask (the reference draws its
+                              mask from torch's Philox stream, not comparable bit for
+                              bit): the published finalizer value fmix32(1) =
+                              0x514e28b7, a scalar pure-Python restatement, the
+                              finalizer's bijectivity on samples, keep rates.
 """
 from __future__ import annotations
 
@@ -432,3 +437,61 @@ def rel_err(y, ref) -> float:
     """Relative Frobenius error ||y - ref|| / ||ref|| (tests/test_accuracy.py:6-7)."""
     y, ref = y.double(), ref.double()
     return float((y - ref).norm() / ref.norm())
+
+
+# ---------------------------------------------------------------------------
+# Attention dropout keep mask: this build's definition (the kernels' device
+# helpers drop_row / drop_pair / drop_keep); the reference passes dropout_p to
+# torch's kernel, whose Philox-based mask is not comparable bit for bit.
+# ---------------------------------------------------------------------------
+
+_U32 = np.uint32
+
+
+def fmix32(h) -> np.ndarray:
+    """MurmurHash3's 32-bit finalizer (A. Appleby, public domain), elementwise on
+    uint32 with wrap-around multiplication."""
+    h = np.array(h, dtype=np.uint64) & 0xFFFFFFFF
+    h ^= h >> 16
+    h = (h * 0x85EBCA6B) & 0xFFFFFFFF
+    h ^= h >> 13
+    h = (h * 0xC2B2AE35) & 0xFFFFFFFF
+    h ^= h >> 16
+    return h.astype(_U32)
+
+
+def dropout_params(p: float):
+    """(thr16, scale) as the C ABI derives them from a float32 dropout_p:
+    thr16 = min(65535, floor(p * 65536 + 0.5)), at least 1 for p > 0;
+    scale = fp32(1 / (1 - p))."""
+    p32 = np.float32(p)
+    if p32 <= 0:
+        return 0, np.float32(1.0)
+    thr = int(min(65535.0, float(p32) * 65536.0 + 0.5))
+    thr = max(thr, 1)
+    return thr, np.float32(1.0) / (np.float32(1.0) - p32)
+
+
+def dropout_keep(seed: int, bh: int, Sq: int, rows, cols, p: float) -> np.ndarray:
+    """Keep mask (len(rows), len(cols)) of query head bh = b * H + h:
+    row = fmix32((bh * Sq + q) ^ seed_lo), u = fmix32(row + (k >> 1) * 0x9E3779B9 +
+    seed_hi), key k kept iff its 16-bit half of u (low half for even k) >= thr16."""
+    thr, _ = dropout_params(p)
+    lo, hi = seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF
+    q = np.asarray(rows, dtype=np.uint64)
+    k = np.asarray(cols, dtype=np.uint64)
+    row = fmix32(((bh * Sq + q) & 0xFFFFFFFF) ^ lo).astype(np.uint64)
+    u = fmix32((row[:, None] + ((k[None, :] >> 1) * 0x9E3779B9) + hi) & 0xFFFFFFFF).astype(np.uint64)
+    half = np.where((k[None, :] & 1) == 1, u >> 16, u & 0xFFFF)
+    return half >= thr
+
+
+def dropout_z(seed: int, B: int, H: int, Sq: int, Sk: int, p: float) -> torch.Tensor:
+    """Z = keep / (1 - p) as float64 (B, H, Sq, Sk): the dropped attention weights are
+    softmax(S) * Z."""
+    _, scale = dropout_params(p)
+    z = np.empty((B, H, Sq, Sk), dtype=np.float64)
+    for b in range(B):
+        for h in range(H):
+            z[b, h] = dropout_keep(seed, b * H + h, Sq, np.arange(Sq), np.arange(Sk), p) * float(scale)
+    return torch.from_numpy(z)

@@ -51,18 +51,22 @@ def test_host_validation_rejects_before_launch():
     assert L.tbf16_gemm_f16(16, 8, 16, 16, 16, 16, 8, 16, 16, None, 16, 8, 99, None) == -1
     # attention: heads not a multiple
     st = (ctypes.c_int64 * 3)(8, 8, 8)
-    assert L.tbf16_attn_fwd(16, 16, 16, 1, 3, 2, 8, 8, 8, st, st, st, None, None, 1.0, 0, 0, 16, None, None, None,
+    assert L.tbf16_attn_fwd(16, 16, 16, 1, 3, 2, 8, 8, 8, st, st, st, None, None, 1.0, 0, 0, 0.0, 0, 16, None, None, None,
                             16, 1 << 20, None) == -1
     assert "multiple of key/value heads" in _err()
     # attention: head dim
-    assert L.tbf16_attn_fwd(16, 16, 16, 1, 2, 2, 8, 8, 264, st, st, st, None, None, 1.0, 0, 0, 16, None, None, None,
+    assert L.tbf16_attn_fwd(16, 16, 16, 1, 2, 2, 8, 8, 264, st, st, st, None, None, 1.0, 0, 0, 0.0, 0, 16, None, None, None,
                             16, 1 << 20, None) == -1
     # workspace too small
-    assert L.tbf16_attn_fwd(16, 16, 16, 1, 2, 2, 8, 8, 64, st, st, st, None, None, 1.0, 0, 0, 16, None, None, None,
+    assert L.tbf16_attn_fwd(16, 16, 16, 1, 2, 2, 8, 8, 64, st, st, st, None, None, 1.0, 0, 0, 0.0, 0, 16, None, None, None,
                             16, 0, None) == -1
     assert "workspace" in _err()
+    # dropout probability outside [0, 1)
+    assert L.tbf16_attn_fwd(16, 16, 16, 1, 2, 2, 8, 8, 64, st, st, st, None, None, 1.0, 0, 0, 1.0, 0, 16, None, None, None,
+                            16, 1 << 20, None) == -1
+    assert "dropout_p" in _err()
     # backward head dim limit
-    assert L.tbf16_attn_bwd(16, 16, 16, 16, 16, 16, 16, 1, 2, 2, 8, 8, 264, st, st, st, st, None, None, 1.0, 0, 5,
+    assert L.tbf16_attn_bwd(16, 16, 16, 16, 16, 16, 16, 1, 2, 2, 8, 8, 264, st, st, st, st, None, None, 1.0, 0, 5, 0.0, 0,
                             16, 16, 16, 16, 16, 16, 1 << 20, None) == -1
 
 

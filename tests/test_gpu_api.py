@@ -275,6 +275,54 @@ def test_autograd_sdpa(dev, name, Hq, Hkv, S, D, causal, qs, gs, vs):
         assert torch.isfinite(o).all() and e < 3e-3, (name, n, e)
 
 
+@pytest.mark.parametrize("causal,D,Hq,Hkv,S", [(False, 64, 4, 4, 384), (True, 128, 8, 4, 520), (True, 256, 2, 2, 300)])
+def test_sdpa_dropout(dev, causal, D, Hq, Hkv, S):
+    """Dropout in the fused kernels against an fp64 reference that applies the
+    oracle's keep mask (this build's hash; the reference's Philox masks are not
+    comparable): softmax(S) * Z with Z = keep / (1 - p), forward and gradients."""
+    from oracle import tbf16_oracle as O
+    from tbf16 import attention
+
+    p = 0.3
+    q = randn(1, Hq, S, D, seed=70).bfloat16().to(dev)
+    k = randn(1, Hkv, S, D, seed=71).bfloat16().to(dev)
+    v = randn(1, Hkv, S, D, seed=72).bfloat16().to(dev)
+    do = randn(1, Hq, S, D, seed=73).bfloat16().to(dev)
+    gqa = Hq != Hkv
+
+    def ref(q, k, v, z):
+        if k.shape[1] != q.shape[1]:
+            k = k.repeat_interleave(q.shape[1] // k.shape[1], 1)
+            v = v.repeat_interleave(q.shape[1] // v.shape[1], 1)
+        s_ = q @ k.transpose(-1, -2) / math.sqrt(q.shape[-1])
+        if causal:
+            s_ = s_.masked_fill(torch.ones(S, S, dtype=torch.bool, device=s_.device).triu(1), float("-inf"))
+        return (torch.softmax(s_, -1) * z) @ v
+
+    # forward with an explicit seed
+    seed = 0x0123_4567_89AB_CDEF
+    z = O.dropout_z(seed, 1, Hq, S, S, p).to(dev)
+    o = attention.attn_forward(q, k, v, None, causal, None, v_exp=13, dropout_p=p, seed=seed)[0]
+    e = rel(o, ref(q.double(), k.double(), v.double(), z))
+    assert torch.isfinite(o).all() and e < 3e-3, ("fwd", e)
+    # the API draws its seed from torch's CPU generator
+    torch.manual_seed(11)
+    seed = attention.dropout_seed()
+    z = O.dropout_z(seed, 1, Hq, S, S, p).to(dev)
+    torch.manual_seed(11)
+    ours = _grads(lambda q, k, v: ag.sdpa(q, k, v, dropout_p=p, is_causal=causal, enable_gqa=gqa), [q, k, v], do)
+    refs = _grads(lambda q, k, v: ref(q, k, v, z), [q.double(), k.double(), v.double()], do.double())
+    for n, a, r in zip(["o", "dq", "dk", "dv"], ours, refs):
+        e = rel(a, r)
+        print(f"dropout causal={causal} D={D} {n}: {e:.3e}")
+        assert torch.isfinite(a).all() and e < 3e-3, (n, e)
+    # dropout_p = 0 is the plain kernel
+    with torch.no_grad():
+        a0 = attention.attn_forward(q, k, v, None, causal, None, v_exp=13, dropout_p=0.0, seed=seed)[0]
+        b0 = sdpa(q, k, v, is_causal=causal, enable_gqa=gqa)
+    assert torch.equal(a0, b0)
+
+
 @pytest.mark.parametrize("kind", ["bool", "float"])
 def test_autograd_sdpa_masks(dev, kind):
     Hq, Hkv, S, D = 8, 4, 1000, 64

@@ -294,3 +294,44 @@ def test_linear_train_bwd_vs_fp64():
     assert O.rel_err(dx, dy.double() @ w.double()) < 3e-3
     assert O.rel_err(dw, dy.double().t() @ x.double()) < 3e-3
     assert O.rel_err(db.float(), dy.double().sum(0)) < 3e-3
+
+
+def test_dropout_mask_pins():
+    """fmix32: the published finalizer value fmix32(1) = 0x514e28b7, a scalar
+    pure-Python restatement, bijectivity on a 2^20 sample; the keep rule: exact
+    thresholds, keep rates within 5 sigma, element-wise scalar restatement."""
+    assert int(O.fmix32(1)) == 0x514E28B7 and int(O.fmix32(0)) == 0
+
+    def fm(h):
+        h &= 0xFFFFFFFF
+        h ^= h >> 16
+        h = (h * 0x85EBCA6B) & 0xFFFFFFFF
+        h ^= h >> 13
+        h = (h * 0xC2B2AE35) & 0xFFFFFFFF
+        return h ^ (h >> 16)
+
+    xs = np.random.default_rng(0).integers(0, 1 << 32, 3000, dtype=np.uint64)
+    assert [int(v) for v in O.fmix32(xs)] == [fm(int(x)) for x in xs]
+    assert len(np.unique(O.fmix32(np.arange(1 << 20)))) == 1 << 20
+
+    assert O.dropout_params(0.0)[0] == 0
+    thr, sc = O.dropout_params(0.25)
+    assert thr == 16384 and sc == np.float32(1.0) / np.float32(0.75)
+    assert O.dropout_params(1e-9)[0] == 1 and O.dropout_params(0.9999999)[0] == 65535
+
+    seed = 0x0123_4567_89AB_CDEF
+    for p in (0.1, 0.5, 0.9):
+        m = O.dropout_keep(seed, 5, 1024, np.arange(1024), np.arange(1024), p)
+        keep = 1.0 - O.dropout_params(p)[0] / 65536.0
+        sigma = math.sqrt(keep * (1 - keep) / m.size)
+        assert abs(m.mean() - keep) < 5 * sigma, (p, m.mean(), keep)
+
+    lo, hi = seed & 0xFFFFFFFF, seed >> 32
+    thr, _ = O.dropout_params(0.3)
+    m = O.dropout_keep(seed, 7, 100, np.arange(100), np.arange(64), 0.3)
+    for qi in (0, 1, 57, 99):
+        row = fm(((7 * 100 + qi) & 0xFFFFFFFF) ^ lo)
+        for kk in (0, 1, 2, 33, 63):
+            u = fm((row + (kk >> 1) * 0x9E3779B9 + hi) & 0xFFFFFFFF)
+            half = (u >> 16) if kk & 1 else (u & 0xFFFF)
+            assert bool(m[qi, kk]) == (half >= thr)

@@ -18,6 +18,18 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Attention dropout parameters: thr16 = round(p * 65536), at least 1 for p > 0 and
+// 0 for no dropout; scale = 1 / (1 - p); the seed's two halves are the mixing words.
+inline void set_dropout(float p, uint64_t seed, uint32_t& lo, uint32_t& hi, uint32_t& thr16, float& scale) {
+  double t = (double)p * 65536.0 + 0.5;
+  if (t > 65535.0) t = 65535.0;
+  thr16 = p > 0.f ? (uint32_t)t : 0u;
+  if (p > 0.f && thr16 == 0u) thr16 = 1u;
+  scale = thr16 ? 1.f / (1.f - p) : 1.f;
+  lo = (uint32_t)seed;
+  hi = (uint32_t)(seed >> 32);
+}
+
 // One (B, H, S, D) bf16 tensor of a multi-tensor head-amax launch: BH = B * H heads,
 // strides sb / sh / ss, nch chunks of rows rows each, maxima into partial[bh * nch + c].
 struct AmaxSeg {

@@ -68,6 +68,10 @@ struct FwdParams {
   uint16_t* o16;
   int32_t* exps;
   int pair;  // causal: block x handles query tiles ntiles-1-x and x (balanced work per block)
+  // dropout (DROP kernels): keep iff the hashed 16-bit value >= drop_thr, kept
+  // weights scaled by drop_scale = 1 / (1 - p)
+  uint32_t drop_lo, drop_hi, drop_thr;
+  float drop_scale;
 };
 
 __device__ __forceinline__ int perm16(int key) {  // swap bits 2 and 3 of a key index
@@ -228,7 +232,7 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
 // Forward kernel: NW waves, 32 query rows each (BQ = 32 * NW), 64-key tiles
 // staged in two LDS stages by direct global -> LDS loads shared out over all
 // waves. NW = 8: two waves per SIMD, one block per CU; NW = 4: two blocks per CU.
-template <int DP, int NW, bool CAUSAL, bool HAS_BIAS>
+template <int DP, int NW, bool CAUSAL, bool HAS_BIAS, bool DROP>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(DP > 128 ? 1 : 2, DP > 128 ? 1 : 2))) void
 attn_fwd_kernel(FwdParams p) {
   constexpr int NT = NW * 64, BQW = 32 * NW;
@@ -238,8 +242,8 @@ attn_fwd_kernel(FwdParams p) {
   constexpr int KBYTES = BKV * DP * 2;
   constexpr int STAGE = KBYTES + DP * 128;
   // V^T fragments read during the QK product (registers allow it up to DP = 128
-  // without the bias rows)
-  constexpr bool VPRE = DP <= 128 && !HAS_BIAS;
+  // without the bias rows or the dropout hashing)
+  constexpr bool VPRE = DP <= 128 && !HAS_BIAS && !DROP;
   // K and V^T tiles go global -> LDS directly, 1 KB per wave instruction: BPW
   // such blocks per wave per tile, the first KPW of them K, the rest V^T
   constexpr int KBLK = KBYTES / 1024, NBLK = STAGE / 1024;
@@ -274,6 +278,7 @@ attn_fwd_kernel(FwdParams p) {
     const int q0 = qt * BQW;
     // ---- Q fragments in registers (fp16, scaled by 2^a) ----
     const int qrow = q0 + wave * 32 + fr;
+    const uint32_t drow = DROP ? drop_row((uint32_t)bh * (uint32_t)p.Sq + (uint32_t)qrow, p.drop_lo) : 0u;
     half8 qf[KS];
     {
       const uint16_t* qp = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)min(qrow, p.Sq - 1) * p.q_ss;
@@ -453,6 +458,12 @@ attn_fwd_kernel(FwdParams p) {
           const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r + 1], c, mneg));
           pk[kh][r >> 1] = pack_f16(p0, p1);
           lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pk[kh][r >> 1]), ones, lsum, false);
+          if constexpr (DROP) {  // l keeps the undropped weights; the PV product gets the dropped ones
+            const int key = key0 + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);  // even
+            const uint32_t u = drop_pair(drow, key, p.drop_hi);
+            pk[kh][r >> 1] = pack_f16(drop_keep(u, key, p.drop_thr) ? p0 * p.drop_scale : 0.f,
+                                      drop_keep(u, key + 1, p.drop_thr) ? p1 * p.drop_scale : 0.f);
+          }
         }
       l_run += lsum;
       // O^T += V^T P^T over four 16-key steps
@@ -565,12 +576,23 @@ WsLayout fwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64
 
 template <int DP, int NW>
 int launch_fwd_nw(const FwdParams& p, bool causal, bool has_bias, dim3 grid, hipStream_t st) {
-  if (causal) {
-    if (has_bias) attn_fwd_kernel<DP, NW, true, true><<<grid, NW * 64, 0, st>>>(p);
-    else attn_fwd_kernel<DP, NW, true, false><<<grid, NW * 64, 0, st>>>(p);
+  // dropout kernels exist for 4-wave blocks only (the launcher picks those)
+  if (p.drop_thr) {
+    if constexpr (NW == 4) {
+      if (causal) {
+        if (has_bias) attn_fwd_kernel<DP, 4, true, true, true><<<grid, 256, 0, st>>>(p);
+        else attn_fwd_kernel<DP, 4, true, false, true><<<grid, 256, 0, st>>>(p);
+      } else {
+        if (has_bias) attn_fwd_kernel<DP, 4, false, true, true><<<grid, 256, 0, st>>>(p);
+        else attn_fwd_kernel<DP, 4, false, false, true><<<grid, 256, 0, st>>>(p);
+      }
+    }
+  } else if (causal) {
+    if (has_bias) attn_fwd_kernel<DP, NW, true, true, false><<<grid, NW * 64, 0, st>>>(p);
+    else attn_fwd_kernel<DP, NW, true, false, false><<<grid, NW * 64, 0, st>>>(p);
   } else {
-    if (has_bias) attn_fwd_kernel<DP, NW, false, true><<<grid, NW * 64, 0, st>>>(p);
-    else attn_fwd_kernel<DP, NW, false, false><<<grid, NW * 64, 0, st>>>(p);
+    if (has_bias) attn_fwd_kernel<DP, NW, false, true, false><<<grid, NW * 64, 0, st>>>(p);
+    else attn_fwd_kernel<DP, NW, false, false, false><<<grid, NW * 64, 0, st>>>(p);
   }
   TB_LAUNCH_CHECK("attn_fwd");
   return 0;
@@ -592,7 +614,7 @@ int launch_fwd_dp(FwdParams p, bool causal, bool has_bias, hipStream_t st, int n
   const bool pair = causal && tiles4 >= 2 * p.B * p.H && tiles8 < 384 && nw_override <= 0 &&
                     getenv("TBF16_ATTN_NOPAIR") == nullptr;
   int nw = nw_override > 0 ? nw_override : pair ? 4 : (tiles8 >= 128 ? 8 : 4);
-  if (DP > 128) nw = 4;
+  if (DP > 128 || p.drop_thr) nw = 4;
   const int64_t ntiles = cdiv(p.Sq, nw == 8 ? 256 : 128);
   p.pair = pair && nw == 4;
   const dim3 grid(p.B * p.H, (unsigned)(p.pair ? cdiv(ntiles, 2) : ntiles));
@@ -619,8 +641,8 @@ extern "C" size_t tbf16_attn_fwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int
 extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t Hkv,
                               int64_t Sq, int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
                               const int64_t* v_strides, const void* bias, const int64_t* bias_strides, float scale,
-                              int causal, int v_exp, void* o, float* lse, void* o16, int32_t* exps, void* ws,
-                              int64_t ws_bytes, void* stream) {
+                              int causal, int v_exp, float dropout_p, uint64_t seed, void* o, float* lse, void* o16,
+                              int32_t* exps, void* ws, int64_t ws_bytes, void* stream) {
   TB_CHECK(B >= 0 && H > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0, "attn_fwd: bad shape");
   TB_CHECK(H % Hkv == 0, "attn_fwd: query heads must be a multiple of key/value heads");
   TB_CHECK(D > 0 && D % 8 == 0 && D <= 256, "attn_fwd: head dim must be a multiple of 8 up to 256");
@@ -630,6 +652,7 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   if (int rc = check_bhsd("attn_fwd", "v", v, v_strides, D)) return rc;
   TB_CHECK(o != nullptr && aligned16(o) && (o16 == nullptr || aligned16(o16)), "attn_fwd: bad output");
   if (bias) TB_CHECK(bias_strides != nullptr, "attn_fwd: bias strides missing");
+  TB_CHECK(dropout_p >= 0.f && dropout_p < 1.f, "attn_fwd: dropout_p must be in [0, 1)");
   const WsLayout w = fwd_ws(B, H, Hkv, Sq, Sk, D);
   TB_CHECK(ws != nullptr && ws_bytes >= (int64_t)w.total, "attn_fwd: workspace too small");
   if (B == 0 || Sq == 0) return 0;
@@ -671,6 +694,7 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   p.o16 = (uint16_t*)o16;
   p.exps = exps;
   p.pair = 0;
+  set_dropout(dropout_p, seed, p.drop_lo, p.drop_hi, p.drop_thr, p.drop_scale);
   char* wsb = reinterpret_cast<char*>(ws);
   p.ex = reinterpret_cast<int32_t*>(wsb + w.off_ex);
   p.k16 = reinterpret_cast<uint16_t*>(wsb + w.off_k16);

@@ -68,6 +68,9 @@ struct BwdParams {
   int32_t* exps_out;  // {e, G}
   int32_t* overflow;
   uint16_t *dq, *dk, *dv;
+  // dropout of the forward pass (DROP kernels regenerate its keep mask)
+  uint32_t drop_lo, drop_hi, drop_thr;
+  float drop_scale;
 };
 
 
@@ -189,13 +192,16 @@ __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
 // dO16 tiles sit in LDS once, row-major: they are the A operand of S = Q K^T and
 // dP = dO V^T (lane = ONE key, 16 queries), and their transposes for dV += P^T dO
 // and dK += dS^T Q come from ds_read_b64_tr_b16, so P and dS feed the MFMAs
-// straight from registers. Without a bias a wave stays within 256 registers and
-// two blocks share a CU.
+// straight from registers. Without a bias or dropout (and at DP <= 128) a wave
+// stays within 256 registers and two blocks share a CU.
 // PART 0 accumulates dK and dV together; for DP = 256 (whose two accumulator
 // sets and K fragments exceed a wave's 512 registers) PART 1 accumulates dV and
 // PART 2 dK, in two launches that each recompute S.
-template <int DP, bool CAUSAL, bool HAS_BIAS, int PART>
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS || DP > 128 ? 1 : 2, HAS_BIAS || DP > 128 ? 1 : 2))) void
+// DROP: the forward's dropout mask regenerated from (seed, row, key): dV takes
+// P o Z and dS = P o (Z o dP - delta), Z = keep / (1 - p).
+template <int DP, bool CAUSAL, bool HAS_BIAS, int PART, bool DROP>
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS || DROP || DP > 128 ? 1 : 2,
+                                                                     HAS_BIAS || DROP || DP > 128 ? 1 : 2))) void
 dkdv_kernel(BwdParams p) {
   constexpr bool WANT_DV = PART != 2, WANT_DK = PART != 1;
   constexpr int BQ = 32, BK = 128;
@@ -214,6 +220,7 @@ dkdv_kernel(BwdParams p) {
   __shared__ __align__(1024) uint8_t sst1[STG];
   __shared__ __align__(16) float s_lse[2][BQ];
   __shared__ __align__(16) float s_delta[2][BQ];
+  __shared__ __align__(16) uint32_t s_drow[DROP ? 2 : 1][BQ];  // dropout row hashes
 
   const int tid = threadIdx.x, lane = tid & 63, fr = lane & 31, fk = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -271,6 +278,7 @@ dkdv_kernel(BwdParams p) {
     voff[i] = (row * DP + lch * 8) * 2;
   }
   float rl = INFINITY, rdl = 0.f;
+  uint32_t rdr = 0u;
   auto tile_src = [&](int it, int& bh, int& q0) {
     const int h = hk * group + it / (nqt - qt0);
     q0 = (qt0 + it % (nqt - qt0)) * BQ;
@@ -283,6 +291,7 @@ dkdv_kernel(BwdParams p) {
       const int qi = q0 + tid;
       rl = qi < p.Sq ? p.lse[(int64_t)bh * p.Sq + qi] : INFINITY;
       rdl = qi < p.Sq ? p.delta[(int64_t)bh * p.Sq + qi] : 0.f;
+      if constexpr (DROP) rdr = drop_row((uint32_t)bh * (uint32_t)p.Sq + (uint32_t)qi, p.drop_lo);
     }
     const int64_t row0 = ((int64_t)bh * p.Sqp + q0) * DP;
     // blocks [0, QBLK) of a stage hold Q16 rows, the rest dO16 rows; a wave's
@@ -296,6 +305,7 @@ dkdv_kernel(BwdParams p) {
     if (tid < BQ) {
       s_lse[stg][tid] = rl;
       s_delta[stg][tid] = rdl;
+      if constexpr (DROP) s_drow[stg][tid] = rdr;
     }
   };
 
@@ -369,14 +379,24 @@ dkdv_kernel(BwdParams p) {
       const float4 l4 = *reinterpret_cast<const float4*>(&s_lse[stg][ql0]);
       const float4 d4 = *reinterpret_cast<const float4*>(&s_delta[stg][ql0]);
       const float lse4[4] = {l4.x, l4.y, l4.z, l4.w}, del4[4] = {d4.x, d4.y, d4.z, d4.w};
-      float pv[4], dsv[4];
+      float pv[4], dsv[4], pz[4];
+      uint4 dr4 = make_uint4(0, 0, 0, 0);
+      if constexpr (DROP) dr4 = *reinterpret_cast<const uint4*>(&s_drow[DROP ? stg : 0][ql0]);
+      const uint32_t dr[4] = {dr4.x, dr4.y, dr4.z, dr4.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         pv[j] = __builtin_amdgcn_exp2f(fmaf(sacc[4 * i + j], cs, -lse4[j]));
-        dsv[j] = WANT_DK ? pv[j] * (pacc[4 * i + j] - del4[j]) : 0.f;
+        float dpj = WANT_DK ? pacc[4 * i + j] : 0.f;
+        pz[j] = pv[j];
+        if constexpr (DROP) {
+          const bool keep = drop_keep(drop_pair(dr[j], key, p.drop_hi), key, p.drop_thr);
+          pz[j] = keep ? pv[j] * p.drop_scale : 0.f;
+          dpj = keep ? dpj * p.drop_scale : 0.f;
+        }
+        dsv[j] = WANT_DK ? pv[j] * (dpj - del4[j]) : 0.f;
       }
-      pp[2 * i] = pack_f16(pv[0], pv[1]);
-      pp[2 * i + 1] = pack_f16(pv[2], pv[3]);
+      pp[2 * i] = pack_f16(pz[0], pz[1]);
+      pp[2 * i + 1] = pack_f16(pz[2], pz[3]);
       ds[2 * i] = pack_f16(dsv[0], dsv[1]);
       ds[2 * i + 1] = pack_f16(dsv[2], dsv[3]);
     }
@@ -465,7 +485,7 @@ dkdv_kernel(BwdParams p) {
 // a private LDS region instead of registers, and K/V arrive in 32-key tiles
 // (double-buffered, direct global -> LDS loads), which keeps a wave within 256
 // registers.
-template <int DP, bool CAUSAL, bool HAS_BIAS>
+template <int DP, bool CAUSAL, bool HAS_BIAS, bool DROP>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS || DP > 128 ? 1 : 2, HAS_BIAS || DP > 128 ? 1 : 2))) void
 dq_kernel(BwdParams p) {
   constexpr int BQ = 128, BKV = 32;
@@ -508,6 +528,7 @@ dq_kernel(BwdParams p) {
   }
   const float lse_q = qrow < p.Sq ? p.lse[(int64_t)bh * p.Sq + qrow] : INFINITY;
   const float delta_q = qrow < p.Sq ? p.delta[(int64_t)bh * p.Sq + qrow] : 0.f;
+  const uint32_t drow = DROP ? drop_row((uint32_t)bh * (uint32_t)p.Sq + (uint32_t)qrow, p.drop_lo) : 0u;
   floatx16 dq[DB];
 #pragma unroll
   for (int i = 0; i < DB; ++i)
@@ -587,7 +608,14 @@ dq_kernel(BwdParams p) {
       for (int r = 0; r < 16; r += 2) {
         const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[r], cs, -lse_q));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[r + 1], cs, -lse_q));
-        ds[r >> 1] = pack_f16(p0 * (pacc[r] - delta_q), p1 * (pacc[r + 1] - delta_q));
+        float dp0 = pacc[r], dp1 = pacc[r + 1];
+        if constexpr (DROP) {  // dS = P o (Z o dP - delta)
+          const int kk = kb0 + 8 * (r >> 2) + 4 * fk + (r & 3);  // even
+          const uint32_t u = drop_pair(drow, kk, p.drop_hi);
+          dp0 = drop_keep(u, kk, p.drop_thr) ? dp0 * p.drop_scale : 0.f;
+          dp1 = drop_keep(u, kk + 1, p.drop_thr) ? dp1 * p.drop_scale : 0.f;
+        }
+        ds[r >> 1] = pack_f16(p0 * (dp0 - delta_q), p1 * (dp1 - delta_q));
       }
 #pragma unroll
       for (int kq = 0; kq < 2; ++kq) {
@@ -671,22 +699,28 @@ template <int DP>
 int launch_bwd_dp(const BwdParams& p, bool causal, bool has_bias, hipStream_t st) {
   dim3 g_kv((unsigned)(p.B * p.Hkv), (unsigned)cdiv(p.Sk, 128));
   dim3 g_q((unsigned)(p.B * p.H), (unsigned)cdiv(p.Sq, 128));
-#define LAUNCH(C, HB)                                        \
-  if constexpr (DP > 128) {                                  \
-    dkdv_kernel<DP, C, HB, 1><<<g_kv, NTH, 0, st>>>(p);      \
-    TB_LAUNCH_CHECK("attn_bwd/dv");                          \
-    dkdv_kernel<DP, C, HB, 2><<<g_kv, NTH, 0, st>>>(p);      \
-    TB_LAUNCH_CHECK("attn_bwd/dk");                          \
-  } else {                                                   \
-    dkdv_kernel<DP, C, HB, 0><<<g_kv, NTH, 0, st>>>(p);      \
-    TB_LAUNCH_CHECK("attn_bwd/dkdv");                        \
-  }                                                          \
-  dq_kernel<DP, C, HB><<<g_q, NTH, 0, st>>>(p);              \
+#define LAUNCH(C, HB, DR)                                        \
+  if constexpr (DP > 128) {                                      \
+    dkdv_kernel<DP, C, HB, 1, DR><<<g_kv, NTH, 0, st>>>(p);      \
+    TB_LAUNCH_CHECK("attn_bwd/dv");                              \
+    dkdv_kernel<DP, C, HB, 2, DR><<<g_kv, NTH, 0, st>>>(p);      \
+    TB_LAUNCH_CHECK("attn_bwd/dk");                              \
+  } else {                                                       \
+    dkdv_kernel<DP, C, HB, 0, DR><<<g_kv, NTH, 0, st>>>(p);      \
+    TB_LAUNCH_CHECK("attn_bwd/dkdv");                            \
+  }                                                              \
+  dq_kernel<DP, C, HB, DR><<<g_q, NTH, 0, st>>>(p);              \
   TB_LAUNCH_CHECK("attn_bwd/dq");
-  if (causal) {
-    if (has_bias) { LAUNCH(true, true) } else { LAUNCH(true, false) }
+  if (p.drop_thr) {
+    if (causal) {
+      if (has_bias) { LAUNCH(true, true, true) } else { LAUNCH(true, false, true) }
+    } else {
+      if (has_bias) { LAUNCH(false, true, true) } else { LAUNCH(false, false, true) }
+    }
+  } else if (causal) {
+    if (has_bias) { LAUNCH(true, true, false) } else { LAUNCH(true, false, false) }
   } else {
-    if (has_bias) { LAUNCH(false, true) } else { LAUNCH(false, false) }
+    if (has_bias) { LAUNCH(false, true, false) } else { LAUNCH(false, false, false) }
   }
 #undef LAUNCH
   return 0;
@@ -702,11 +736,12 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
                               const void* dout, const int32_t* exps_fwd, int64_t B, int64_t H, int64_t Hkv, int64_t Sq,
                               int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
                               const int64_t* v_strides, const int64_t* do_strides, const void* bias,
-                              const int64_t* bias_strides, float scale, int causal, int t_do, void* dq, void* dk,
-                              void* dv, int32_t* exps_out, int32_t* overflow, void* ws, int64_t ws_bytes,
-                              void* stream) {
+                              const int64_t* bias_strides, float scale, int causal, int t_do, float dropout_p,
+                              uint64_t seed, void* dq, void* dk, void* dv, int32_t* exps_out, int32_t* overflow,
+                              void* ws, int64_t ws_bytes, void* stream) {
   TB_CHECK(B >= 0 && H > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0 && H % Hkv == 0, "attn_bwd: bad shape");
   TB_CHECK(D > 0 && D % 8 == 0 && D <= 256, "attn_bwd: head dim must be a multiple of 8 up to 256");
+  TB_CHECK(dropout_p >= 0.f && dropout_p < 1.f, "attn_bwd: dropout_p must be in [0, 1)");
   TB_CHECK(q && k && v && o16 && lse && dout && exps_fwd && dq && dk && dv && exps_out && overflow,
            "attn_bwd: null argument");
   TB_CHECK(q_strides && k_strides && v_strides && do_strides, "attn_bwd: strides missing");
@@ -735,6 +770,7 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
   p.bias_sb = bias ? bias_strides[0] : 0; p.bias_sh = bias ? bias_strides[1] : 0; p.bias_sq = bias ? bias_strides[2] : 0;
   p.B = (int)B; p.H = (int)H; p.Hkv = (int)Hkv; p.Sq = (int)Sq; p.Sk = (int)Sk; p.D = (int)D;
   p.scale = scale; p.scale_log2 = scale * kLog2e; p.causal = causal; p.t_do = t_do;
+  set_dropout(dropout_p, seed, p.drop_lo, p.drop_hi, p.drop_thr, p.drop_scale);
   p.part_do = part; p.nch_do = (int)w.nch;
   p.delta = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_delta);
   p.exps_out = exps_out; p.overflow = overflow;

@@ -200,6 +200,32 @@ __device__ __forceinline__ float sum_xor32(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// ---- attention dropout --------------------------------------------------------
+
+// Keep decisions for attention dropout from a counter-based hash, so the forward
+// and the backward regenerate the same mask without storing it. MurmurHash3's
+// 32-bit finalizer (fmix32; A. Appleby, public domain) mixes
+//   row(bh, q) = fmix32((bh * Sq + q) ^ seed_lo)                 (once per row)
+//   u(q, k)    = fmix32(row + (k >> 1) * 0x9E3779B9 + seed_hi)   (one per key pair)
+// and key k keeps iff its 16-bit half of u (low half for even k) is >= thr16,
+// thr16 = round(p * 65536): P(keep) = 1 - thr16 / 65536. Kept weights are scaled
+// by 1 / (1 - p). The host oracle restates these steps.
+__device__ __forceinline__ uint32_t fmix32(uint32_t h) {
+  h ^= h >> 16;
+  h *= 0x85ebca6bu;
+  h ^= h >> 13;
+  h *= 0xc2b2ae35u;
+  h ^= h >> 16;
+  return h;
+}
+__device__ __forceinline__ uint32_t drop_row(uint32_t bh_sq_q, uint32_t seed_lo) { return fmix32(bh_sq_q ^ seed_lo); }
+__device__ __forceinline__ uint32_t drop_pair(uint32_t row, int k, uint32_t seed_hi) {
+  return fmix32(row + (uint32_t)(k >> 1) * 0x9E3779B9u + seed_hi);
+}
+__device__ __forceinline__ bool drop_keep(uint32_t u, int k, uint32_t thr16) {
+  return ((k & 1) ? (u >> 16) : (u & 0xFFFFu)) >= thr16;
+}
+
 // ---- LDS tiles ---------------------------------------------------------------
 
 // Byte offset of 16-byte chunk `chunk` of row `row` in a row-major DP-wide fp16 LDS

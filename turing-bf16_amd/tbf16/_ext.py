@@ -26,6 +26,7 @@ I = ctypes.c_int
 I64 = ctypes.c_int64
 F = ctypes.c_float
 SZ = ctypes.c_size_t
+U64 = ctypes.c_uint64
 PI64 = ctypes.POINTER(ctypes.c_int64)
 
 # name -> (restype, argtypes); mirrors include/tbf16_hip.h
@@ -44,11 +45,11 @@ _SIGS = {
     "tbf16_head_amax": (I, [P, I, I64, I64, I64, I64, I64, I64, I64, P, P]),
     "tbf16_head_scale_cast": (I, [P, I, I64, I64, I64, I64, I64, I64, I64, P, I64, I64, P, I, P]),
     "tbf16_attn_fwd_ws_bytes": (SZ, [I64, I64, I64, I64, I64, I64]),
-    "tbf16_attn_fwd": (I, [P, P, P, I64, I64, I64, I64, I64, I64, PI64, PI64, PI64, P, PI64, F, I, I, P, P, P, P,
+    "tbf16_attn_fwd": (I, [P, P, P, I64, I64, I64, I64, I64, I64, PI64, PI64, PI64, P, PI64, F, I, I, F, U64, P, P, P, P,
                            P, I64, P]),
     "tbf16_attn_bwd_ws_bytes": (SZ, [I64, I64, I64, I64, I64, I64]),
     "tbf16_attn_bwd": (I, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, PI64, PI64, PI64, PI64, P, PI64, F,
-                           I, I, P, P, P, P, P, P, I64, P]),
+                           I, I, F, U64, P, P, P, P, P, P, I64, P]),
 }
 
 

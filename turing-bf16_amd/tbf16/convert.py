@@ -77,21 +77,15 @@ class TrainLinear(nn.Linear):
 _native_sdpa = F.scaled_dot_product_attention
 
 
-def _dropout_of(args, kwargs):
-    if "dropout_p" in kwargs:
-        return kwargs["dropout_p"]
-    return args[1] if len(args) > 1 else 0.0
-
-
 def _sdpa(query, key, value, *args, **kwargs):  # torch's parameter names: callers pass them as keywords
     """Router of tbf16/convert.py:79-88. bf16 4-D inputs with D <= 256 (multiple of 8)
-    and at least MIN_QUERY_ROWS query rows go to tbf16; dropout (not in the fused
-    kernel) and everything else run natively."""
+    and at least MIN_QUERY_ROWS query rows go to tbf16 (dropout included, as the
+    reference routes it); everything else runs natively."""
     q, k, v = query, key, value
     if q.is_cuda and torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
         q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
     if (q.dtype == k.dtype == v.dtype == torch.bfloat16 and q.is_cuda and q.dim() == 4 and q.shape[-1] <= 256
-            and q.shape[-1] % 8 == 0 and q.shape[-2] >= MIN_QUERY_ROWS and not _dropout_of(args, kwargs)):
+            and q.shape[-1] % 8 == 0 and q.shape[-2] >= MIN_QUERY_ROWS):
         if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
             return autograd.sdpa(q, k, v, *args, **kwargs)
         return sdpa(q, k, v, *args, **kwargs)

@@ -47,9 +47,8 @@ class TuringBF16Mode(TorchFunctionMode):
             kwargs = dict(kwargs)  # q, k, v may come as keywords (diffusers passes query=, key=, value=)
             q, k, v = (args[i] if i < len(args) else kwargs.pop(n) for i, n in enumerate(("query", "key", "value")))
             rest = args[3:]
-            dropout = kwargs.get("dropout_p", rest[1] if len(rest) > 1 else 0.0)
             if (_ok(q, k, v) and not torch.is_grad_enabled() and q.dim() == 4 and q.shape[-1] <= 256
-                    and q.shape[-1] % 8 == 0 and q.shape[-2] >= self.min_rows and not dropout):
+                    and q.shape[-1] % 8 == 0 and q.shape[-2] >= self.min_rows):
                 self.stats["sdpa"] += 1
                 return sdpa(q, k, v, *rest, **kwargs)
             self.stats["sdpa_native"] += 1
