@@ -99,7 +99,8 @@ def test_quantize_rows_t_and_cols_t_bit_exact(dev):
 # ---- MFMA layout and epilogue: exact small-integer GEMMs -------------------------
 
 # tiled configurations 0-4 take any M; skinny ones (5-8) M <= 32 or 64
-GEMM_CFG_M = {0: 300, 1: 300, 2: 300, 3: 300, 4: 300, 5: 29, 6: 29, 7: 61, 8: 61, 9: 300, 10: 300, 11: 300, 12: 300}
+GEMM_CFG_M = {0: 300, 1: 300, 2: 300, 3: 300, 4: 300, 5: 29, 6: 29, 7: 61, 8: 61, 9: 300, 10: 300, 11: 300, 12: 300,
+              13: 29}
 
 
 @pytest.mark.parametrize("cfg", sorted(GEMM_CFG_M))

@@ -681,13 +681,15 @@ struct TileCfg {
 // 10: 256x128, 8 waves of 64x64, 1 set
 // 11: 256x64, 8 waves of 64x32, 2 sets
 // and 12: 128x64, 4 waves of 64x32, k 64, 3 sets, 3 stages
+// Skinny, M <= 32: 13: 64 b rows per block, 8 waves splitting K, 3 chunks in flight
 constexpr TileCfg kCfgs[] = {{256, 256, 32}, {128, 128, 64}, {64, 64, 64},       {128, 128, 64},    {256, 256, 32},
                              {32, 32, 64, true}, {32, 32, 64, true}, {64, 32, 64, true}, {64, 64, 64, true},
-                             {256, 256, 64}, {256, 128, 64}, {256, 64, 64}, {128, 64, 64}};
-constexpr int kNumCfgs = 13;
+                             {256, 256, 64}, {256, 128, 64}, {256, 64, 64}, {128, 64, 64}, {32, 64, 64, true}};
+constexpr int kNumCfgs = 14;
 
 // Configuration choice, fitted to measurements on MI355X (256 CUs): for M <= 64
-// with enough b rows for 160 blocks, the 64-row skinny block up to M = 32 and
+// with enough b rows for 160 blocks, the 64-row skinny block (8 waves splitting
+// K, 3 chunks in flight: 17.6 -> 16.4 us at M = 16, K = 2560, N = 10240) up to M = 32 and
 // the LDS-staged 64x64 tile above (every skinny block re-reads all of a, which
 // costs more than the weights from M ~ 40 on). Otherwise the tile that maximises
 // eff x (blocks / whole rounds of 256 blocks) x (M / M rounded up to the tile):
@@ -695,7 +697,7 @@ constexpr int kNumCfgs = 13;
 // mostly empty row of tiles wastes CUs.
 int pick_cfg(int64_t M, int64_t N) {
   if (M <= 64) {
-    if (cdiv(N, 64) >= 160) return M <= 32 ? 8 : 2;
+    if (cdiv(N, 64) >= 160) return M <= 32 ? 13 : 2;
     return M <= 32 ? 6 : 7;
   }
   constexpr int64_t kCUs = 256;
@@ -761,6 +763,7 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
     case 5: SKINNY(1, 1, 4, 4, false); break;
     case 6: SKINNY(1, 1, 4, 4, true); break;
     case 7: SKINNY(1, 2, 4, 3, true); break;
+    case 13: SKINNY(2, 1, 8, 3, true); break;
     default: SKINNY(2, 2, 4, 2, true); break;
 #undef SKINNY
 #undef CFG
