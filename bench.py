@@ -11,7 +11,8 @@ over K steps timed with HIP events between two synchronizations.
 Also measured (same JSON line): the 16k-token causal scaled attention forward
 (configs[3]) and its 4k variant, the small-M decode sweep in HBM GB/s (configs[2],
 weights rotated over > 256 MB so the MALL cannot hold them), and the training
-step of configs[4]. `roofline` prices the dominant kernel (the GEMM) against the
+step of configs[4], and a 3x3 scaled convolution beside torch's native bf16 and fp16
+convolutions (the conv.py path; not a BASELINE config). `roofline` prices the dominant kernel (the GEMM) against the
 dense fp16 MFMA peak from its own event-timed launches; `cpu_baseline` times the
 oracle's restatement of the same workload on the host cores.
 """
@@ -193,6 +194,42 @@ def bench_train(iters: int):
             "step_tflops": round((lin_fl + att_fl) / ((lin_ms + att_ms) * 1e-3) / 1e12, 1)}
 
 
+def bench_conv(iters: int):
+    """A VAE-decoder-shaped 3x3 convolution (1, 512, 128, 128) -> 512 channels, bias,
+    NCHW and channels-last: tbf16's scaled path (per-sample input pass, MIOpen fp16
+    convolution, epilogue) beside torch's native bf16 and fp16 convolutions."""
+    import copy
+    import torch
+    import torch.nn as nn
+    import torch.nn.functional as F
+    from tbf16.conv import convert_conv
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(0)
+    out = {}
+    for cl in (False, True):
+        conv = nn.Conv2d(512, 512, 3, padding=1).to(dev).bfloat16()
+        x = torch.randn(1, 512, 128, 128, generator=g).bfloat16().to(dev)
+        if cl:
+            conv = conv.to(memory_format=torch.channels_last)
+            x = x.to(memory_format=torch.channels_last)
+        w, b = conv.weight.detach(), conv.bias.detach()
+        tc = convert_conv(copy.deepcopy(conv))
+        xh, wh, bh = x.half(), w.half(), b.half()
+        fl = 2.0 * 512 * 512 * 9 * 128 * 128
+        r = {}
+        with torch.no_grad():
+            for name, fn in (("tbf16", lambda: tc(x)), ("native_bf16", lambda: F.conv2d(x, w, b, 1, 1)),
+                             ("native_fp16", lambda: F.conv2d(xh, wh, bh, 1, 1))):
+                for _ in range(3):
+                    fn()
+                ms = _events_time(fn, iters)
+                r[f"{name}_us"] = round(ms * 1e3, 1)
+                r[f"{name}_tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
+        out["channels_last" if cl else "nchw"] = r
+    return out
+
+
 def library_ceiling():
     """torch's own fp16 kernels on the same shapes (hipBLASLt GEMM, torch SDPA): the
     library ceiling the scaled path is compared with. Plain fp16 inputs, no scaling."""
@@ -270,6 +307,8 @@ def profile_run(what: str):
                 tbf16.sdpa(q, k, v, is_causal=True)
     elif what == "train":
         bench_train(2)
+    elif what == "conv":
+        bench_conv(3)
     else:
         bench_small_m(2)
     torch.cuda.synchronize()
@@ -295,7 +334,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)  # ~30 ms: lets the clocks settle
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline GEMM only")
-    ap.add_argument("--profile", choices=["gemm", "attention", "small_m", "train"], default=None,
+    ap.add_argument("--profile", choices=["gemm", "attention", "small_m", "train", "conv"], default=None,
                     help="run a few launches of one workload for rocprofv3 and exit (no JSON); 'gemm' also runs a "
                          "256 MiB device copy that calibrates FETCH_SIZE / WRITE_SIZE")
     a = ap.parse_args()
@@ -322,6 +361,8 @@ def main():
         print(f"[bench] small-M {extras['small_m_decode']}", file=sys.stderr, flush=True)
         extras["train_step"] = bench_train(5)
         print(f"[bench] train {extras['train_step']}", file=sys.stderr, flush=True)
+        extras["conv_3x3"] = bench_conv(30)
+        print(f"[bench] conv {extras['conv_3x3']}", file=sys.stderr, flush=True)
     achieved = g["gemm_tflops"]
     line = {
         "metric": base["metric"],

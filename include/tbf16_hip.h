@@ -112,6 +112,28 @@ int tbf16_head_scale_cast(const void* x, int in_dtype, int64_t B, int64_t H, int
                           int64_t sh, int64_t ss, const int32_t* e, int64_t e_sb, int64_t e_sh, void* y,
                           int out_dtype, void* stream);
 
+/* Scaled convolution input: per-sample exponents and the scaled fp16 copy.
+ * x bf16 holds B samples of n elements each, back to back (a contiguous NC...
+ * or channels-last tensor), 16-byte aligned; x16 fp16 has the same layout.
+ * exps[b] = frexp(max |x[b]|) - t (1 - t for an all-zero or NaN sample, -t for
+ * an infinite one); x16 = fp16(x * 2^-exps[b]) from fp32, one RNE rounding.
+ * ws: tbf16_conv_input_ws_bytes(B, n) bytes of scratch.
+ * Replaces the input half of _scaled_conv_forward (tbf16/conv.py:49-54:
+ * vector_norm, frexp, ldexp, mul). */
+size_t tbf16_conv_input_ws_bytes(int64_t B, int64_t n);
+int tbf16_conv_input(const void* x, int64_t B, int64_t n, int t, int32_t* exps, void* x16, void* ws,
+                     int64_t ws_bytes, void* stream);
+
+/* Scaled convolution epilogue: out = bf16(y16 * (2^exps[b] * ws[o]) + bias[o]),
+ * the scale an fp32 product, the sum rounded to fp32 then to bf16. y16 fp16 and
+ * out bf16 are (B, O, P) contiguous (channels_last = 0) or (B, P, O)
+ * (channels_last = 1), P = prod(output spatial), 16-byte aligned; ws fp32 (O,)
+ * inverse weight scales; bias fp32 (O,) or NULL.
+ * Replaces the output half of _scaled_conv_forward (tbf16/conv.py:56-60:
+ * ldexp, mul / addcmul). */
+int tbf16_conv_epilogue(const void* y16, int64_t B, int64_t O, int64_t P, int channels_last, const int32_t* exps,
+                        const float* ws, const float* bias, void* out, void* stream);
+
 /* Scaled attention forward (flash-style, no S x S buffer).
  * Exponents (tbf16/attention.py:267-277): eq/ek = max over heads of frexp(amax),
  * a = clamp(floor((ek - eq) / 2)), ev[b, hkv] = frexp(amax v[b, hkv]) - v_exp.

@@ -29,6 +29,14 @@ How each function is pinned (checked by tests/test_oracle.py):
                               bit): the published finalizer value fmix32(1) =
                               0x514e28b7, a scalar pure-Python restatement, the
                               finalizer's bijectivity on samples, keep rates.
+  conv_sample_exps            amax * 2^-e in [2^(t-1), 2^t) for every normal bf16
+                              amax, math.frexp brute force over bf16 subnormal
+                              maxima, the zero / NaN / inf cases of conv.py:28-31.
+  conv_scale_input            x16 * 2^e == x exactly for elements within fp16's
+                              normal range; torch's RNE cast elsewhere.
+  conv_epilogue               an fp64 -> fp32 -> bf16 numpy restatement (bit level).
+  conv_forward / conv_ref64   exact small-integer convolutions; fp64 rel err bar
+                              of tests/test_conv.py:43 on random inputs.
 """
 from __future__ import annotations
 
@@ -495,3 +503,78 @@ def dropout_z(seed: int, B: int, H: int, Sq: int, Sk: int, p: float) -> torch.Te
         for h in range(H):
             z[b, h] = dropout_keep(seed, b * H + h, Sq, np.arange(Sq), np.arange(Sk), p) * float(scale)
     return torch.from_numpy(z)
+
+
+# ---------------------------------------------------------------------------
+# Scaled convolutions (tbf16/conv.py): per-sample input exponents, the scaled
+# fp16 input, the fp16 convolution (emulated) and the bf16 epilogue.
+# ---------------------------------------------------------------------------
+
+def conv_sample_exps(x: torch.Tensor, t: int) -> np.ndarray:
+    """tbf16/conv.py:28-31,49-50: e[b] = frexp(max |x[b]|) - t, where the max-norm
+    propagates NaN and an amax that is not > 0 (zero or NaN) is taken as 1; an
+    infinite amax has frexp exponent 0."""
+    B = x.shape[0]
+    if B == 0:
+        return np.zeros((0,), dtype=np.int32)
+    amax = x.detach().float().reshape(B, -1).abs().amax(dim=1).numpy()
+    amax = np.where(amax > 0, amax, np.float32(1.0))
+    return (frexp_exp(amax) - t).astype(np.int32)
+
+
+def conv_scale_input(x: torch.Tensor, e) -> torch.Tensor:
+    """tbf16/conv.py:51-54: fp16(x * ldexp(1, -e[b])) with the scale an fp32 power of
+    two (inf for -e >= 128) and one RNE rounding of the fp32 product."""
+    e = np.asarray(e, dtype=np.int32)
+    s = torch.from_numpy(ldexp1(-e)).view((-1,) + (1,) * (x.dim() - 1))
+    return (x.float() * s).half()
+
+
+def conv_epilogue(y16: torch.Tensor, e, ws: torch.Tensor, bias=None) -> torch.Tensor:
+    """tbf16/conv.py:56-60: bf16(y16 * (2^e[b] * ws[o]) + bias[o]): the scale is the fp32
+    product of two powers of two, y16 * scale and the bias add are fp32 operations,
+    the result is rounded once more to bf16."""
+    B, O = y16.shape[:2]
+    view = (B, O) + (1,) * (y16.dim() - 2)
+    scale = (torch.from_numpy(ldexp1(np.asarray(e, dtype=np.int32)))[:, None] * ws.float()[None, :]).view(view)
+    r = y16.float() * scale
+    if bias is not None:
+        r = r + bias.float().view((1, O) + (1,) * (y16.dim() - 2))
+    return r.bfloat16()
+
+
+_CONV_FNS = {1: F.conv1d, 2: F.conv2d, 3: F.conv3d}
+
+
+def conv_weight(w: torch.Tensor):
+    """tbf16/conv.py:89-97: the weight as (fp16 of its shape, fp32 (O,) inverse scales),
+    one max scale per output channel at t = target_exp(C_in / groups * prod(kernel))."""
+    O = w.shape[0]
+    w16, ws = prepare_weight(w.reshape(O, -1))
+    return w16.reshape(w.shape), ws
+
+
+def conv_forward(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None, stride=1, padding=0,
+                 dilation=1, groups=1) -> torch.Tensor:
+    """tbf16/conv.py:39-60 (zero padding) on the CPU: exponents, scaled input, an fp16
+    convolution emulated as the exact (fp64) sum rounded to fp16 -- the library
+    accumulates in fp32, so this is its error up to the fp32 accumulation -- and
+    the epilogue. The input must be batched."""
+    nd = x.dim() - 2
+    t = target_exp(w16[0].numel())
+    e = conv_sample_exps(x, t)
+    x16 = conv_scale_input(x, e)
+    y = _CONV_FNS[nd](x16.double(), w16.double(), None, stride, padding, dilation, groups)
+    return conv_epilogue(y.half(), e, ws, bias)
+
+
+def conv_ref64(x: torch.Tensor, w: torch.Tensor, bias=None, stride=1, padding=0, dilation=1, groups=1,
+               padding_mode: str = "zeros", reversed_padding=None) -> torch.Tensor:
+    """The reference's accuracy oracle (tests/test_conv.py:15-21): the fp64 convolution
+    of the same bf16 input with the dequantized weight."""
+    nd = x.dim() - 2
+    b = None if bias is None else bias.double()
+    if padding_mode != "zeros":
+        xp = F.pad(x.double(), reversed_padding, mode=padding_mode)
+        return _CONV_FNS[nd](xp, w.double(), b, stride, 0, dilation, groups)
+    return _CONV_FNS[nd](x.double(), w.double(), b, stride, padding, dilation, groups)

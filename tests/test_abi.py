@@ -68,6 +68,16 @@ def test_host_validation_rejects_before_launch():
     # backward head dim limit
     assert L.tbf16_attn_bwd(16, 16, 16, 16, 16, 16, 16, 1, 2, 2, 8, 8, 264, st, st, st, st, None, None, 1.0, 0, 5, 0.0, 0,
                             16, 16, 16, 16, 16, 16, 1 << 20, None) == -1
+    # convolution passes: misaligned input, small workspace, null epilogue operand
+    assert L.tbf16_conv_input(18, 2, 64, 0, 16, 16, 16, 1 << 10, None) == -1
+    assert "aligned" in _err()
+    assert L.tbf16_conv_input(16, 2, 64, 0, 16, 16, 16, 0, None) == -1
+    assert "workspace" in _err()
+    assert L.tbf16_conv_epilogue(16, 2, 4, 9, 0, None, 16, None, 16, None) == -1
+    assert "null" in _err()
+    # empty inputs launch nothing and succeed
+    assert L.tbf16_conv_input(None, 0, 64, 0, None, None, None, 0, None) == 0
+    assert L.tbf16_conv_epilogue(None, 0, 4, 9, 0, None, None, None, None, None) == 0
 
 
 def test_workspace_sizes_monotone():
@@ -77,6 +87,7 @@ def test_workspace_sizes_monotone():
     assert 0 < a <= b
     assert L.tbf16_quantize_cols_ws_bytes(8192, 6144) >= 6144 * 4
     assert L.tbf16_attn_bwd_ws_bytes(2, 16, 16, 4096, 4096, 128) >= 2 * 16 * 4096 * 4
+    assert L.tbf16_conv_input_ws_bytes(3, 100000) >= 3 * 4 * 4 and L.tbf16_conv_input_ws_bytes(0, 5) == 0
 
 
 def test_missing_library_raises(monkeypatch, tmp_path):

@@ -335,3 +335,88 @@ def test_dropout_mask_pins():
             u = fm((row + (kk >> 1) * 0x9E3779B9 + hi) & 0xFFFFFFFF)
             half = (u >> 16) if kk & 1 else (u & 0xFFFF)
             assert bool(m[qi, kk]) == (half >= thr)
+
+
+# ---- scaled convolutions (tbf16/conv.py) --------------------------------------------
+
+def _bf16_from_bits(bits, shape):
+    return torch.from_numpy(np.asarray(bits, dtype=np.uint16).astype(np.int16)).view(torch.bfloat16).reshape(shape)
+
+
+@pytest.mark.parametrize("t", [-3, -1, 0])
+def test_conv_sample_exps_pins(t):
+    """Every positive bf16 as a sample's max: normal maxima land in [2^(t-1), 2^t)
+    after scaling by 2^-e; subnormal maxima match math.frexp; zero and NaN samples
+    take amax = 1, infinite ones frexp's 0 (conv.py:28-31,49-50)."""
+    mags = POS_BF16[:0x7F80]  # +0 ... largest finite
+    x = _bf16_from_bits(mags, (len(mags), 1))
+    x = torch.cat([x, -x[:, :1] * 0.5], dim=1)  # second element smaller, negative
+    e = O.conv_sample_exps(x, t)
+    a = bf16_vals(mags).astype(np.float64)
+    normal = (mags >= 0x0080)
+    scaled = a[normal] * np.ldexp(1.0, -e[normal].astype(np.int64))
+    assert np.all(scaled >= 2.0 ** (t - 1)) and np.all(scaled < 2.0 ** t)
+    sub = np.nonzero((mags > 0) & ~normal)[0]
+    assert all(e[i] == math.frexp(float(a[i]))[1] - t for i in sub)
+    assert e[0] == 1 - t  # all-zero sample
+    special = _bf16_from_bits([0x7F80, 0x0000, 0x7FC0, 0x3F80, 0xFF80, 0x3F80], (3, 2))
+    assert O.conv_sample_exps(special, t).tolist() == [-t, 1 - t, -t]  # inf; NaN -> 1 - t; -inf
+    assert O.conv_sample_exps(_bf16_from_bits([0x7FC0, 0x4000], (1, 2)), t).tolist() == [1 - t]
+
+
+def test_conv_scale_input_exact_and_rne():
+    """x16 * 2^e reproduces x exactly for elements inside fp16's normal range, and
+    every element equals torch's RNE cast of the fp32 product."""
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(3, 5, 7, 9, generator=g) * torch.tensor([1e-6, 1.0, 3e4]).view(3, 1, 1, 1)).bfloat16()
+    x[1, 0, 0, :4] = 0.0
+    x[2, 1, 2, 3] = 2e-3  # > 2^14 below the sample max: an fp16 subnormal
+    e = O.conv_sample_exps(x, 0)
+    x16 = O.conv_scale_input(x, e)
+    back = x16.double() * torch.from_numpy(np.ldexp(1.0, e.astype(np.int64))).view(3, 1, 1, 1)
+    normal = x16.float().abs() >= 2.0 ** -14
+    assert torch.equal(back[normal], x.double()[normal])
+    assert x16.float().abs().amax() < 1.0 and x16.float().abs().amax() >= 0.5  # t = 0: [2^-1, 2^0)
+    for b in range(3):
+        ref = (x[b].float() * float(np.ldexp(np.float32(1), -int(e[b])))).half()
+        assert torch.equal(x16[b].view(torch.int16), ref.view(torch.int16))
+
+
+def test_conv_epilogue_bits():
+    """conv_epilogue against a numpy restatement at bit level: exact product in
+    fp64, one rounding to fp32 after the bias add, then RNE to bf16."""
+    g = torch.Generator().manual_seed(4)
+    B, O_, P = 3, 5, 11
+    y16 = (torch.randn(B, O_, P, generator=g) * 300).half()
+    e = np.array([-20, 3, 40], dtype=np.int32)
+    ws = torch.from_numpy(np.ldexp(np.float32(1), np.array([-7, 0, 5, -30, 2])).astype(np.float32))
+    bias = (torch.randn(O_, generator=g) * 100).bfloat16()
+    for bb in (None, bias):
+        out = O.conv_epilogue(y16, e, ws, bb)
+        ex = (y16.double().numpy() * np.ldexp(1.0, e.astype(np.int64))[:, None, None]
+              * ws.double().numpy()[None, :, None])
+        if bb is not None:
+            ex = ex + bb.double().numpy()[None, :, None]
+        ref_bits = O.f32_to_bf16_rne_bits(ex.astype(np.float32))
+        assert np.array_equal(out.view(torch.int16).numpy().astype(np.uint16), ref_bits)
+
+
+def test_conv_forward_exact_integers_and_fp64_bar():
+    """Small-integer inputs and weights: every stage is exact, so the restatement
+    equals the fp64 convolution rounded once to bf16. Random inputs: the reference's
+    bar of 3e-3 (tests/test_conv.py:43), and a transposed weight fails it."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randint(-4, 5, (2, 6, 9, 8), generator=g).bfloat16()
+    w = torch.randint(-3, 4, (7, 6, 3, 3), generator=g).bfloat16()
+    bias = torch.randint(-8, 9, (7,), generator=g).bfloat16()
+    w16, ws = O.conv_weight(w)
+    assert torch.equal((w16.float() * ws.view(-1, 1, 1, 1)).bfloat16(), w)
+    y = O.conv_forward(x, w16, ws, bias, 1, 1)
+    assert torch.equal(y, O.conv_ref64(x, w, bias, 1, 1).bfloat16())
+    x = (torch.randn(2, 16, 12, 10, generator=g) * 7).bfloat16()
+    w = (torch.randn(24, 16, 3, 3, generator=g) * 0.1).bfloat16()
+    w16, ws = O.conv_weight(w)
+    r = O.conv_ref64(x, w, None, 2, 1)
+    assert O.rel_err(O.conv_forward(x, w16, ws, None, 2, 1), r) < 3e-3
+    w16t = w16.transpose(2, 3).contiguous()
+    assert O.rel_err(O.conv_forward(x, w16t, ws, None, 2, 1), r) > 0.1

@@ -44,6 +44,9 @@ _SIGS = {
     "tbf16_gemv": (I, [P, P, I64, I64, I64, P, P, P, P]),
     "tbf16_head_amax": (I, [P, I, I64, I64, I64, I64, I64, I64, I64, P, P]),
     "tbf16_head_scale_cast": (I, [P, I, I64, I64, I64, I64, I64, I64, I64, P, I64, I64, P, I, P]),
+    "tbf16_conv_input_ws_bytes": (SZ, [I64, I64]),
+    "tbf16_conv_input": (I, [P, I64, I64, I, P, P, P, I64, P]),
+    "tbf16_conv_epilogue": (I, [P, I64, I64, I64, I, P, P, P, P, P]),
     "tbf16_attn_fwd_ws_bytes": (SZ, [I64, I64, I64, I64, I64, I64]),
     "tbf16_attn_fwd": (I, [P, P, P, I64, I64, I64, I64, I64, I64, PI64, PI64, PI64, P, PI64, F, I, I, F, U64, P, P, P, P,
                            P, I64, P]),

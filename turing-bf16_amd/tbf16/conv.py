@@ -1,0 +1,136 @@
+"""bf16 convolutions on fp16 MIOpen kernels (tbf16/conv.py of the reference).
+
+The weight gets one exact power-of-two scale per output channel and the input one
+per sample (a convolution mixes positions, so rows cannot be scaled separately);
+the convolution runs in fp16 with fp32 accumulation and the scales are undone in
+one pass that writes bf16. The weight conversion is lossless; the input's is
+lossless for every element within 2^14 of its sample's max (smaller ones become
+fp16 subnormals, far below the output's bf16 rounding).
+
+On MI355X the passes around the convolution are HIP kernels behind the C ABI
+(tbf16_conv_input: per-sample max, exponent and scaled fp16 copy;
+tbf16_conv_epilogue: both scales and the bias in one bf16-writing pass); the fp16
+convolution is MIOpen's, through torch. 1x1 convolutions (stride 1, no padding,
+one group) are per-pixel linear layers and go through scaled_linear, which scales
+each pixel separately. Inference only: inputs that need gradients, or are not
+bf16, run the native convolution on the dequantized weight (conv.py:34-38).
+"""
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ._ext import launch, lib, ptr
+from .ops import _dev_check, _target_exp, prepare_weight, scaled_linear
+
+_CONV = {1: F.conv1d, 2: F.conv2d, 3: F.conv3d}
+_CHANNELS_LAST = {2: torch.channels_last, 3: torch.channels_last_3d}
+
+
+def _sample_major(x: torch.Tensor, nd: int) -> torch.Tensor:
+    """x itself when each sample is one dense run of memory (contiguous, or
+    channels-last for 2-D/3-D) starting 16-byte aligned, else a copy that is."""
+    dense = x.is_contiguous() or (nd in _CHANNELS_LAST and x.is_contiguous(memory_format=_CHANNELS_LAST[nd]))
+    if not dense:
+        x = x.contiguous()
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
+def scale_input(x: torch.Tensor, t: int):
+    """bf16 (B, C, *spatial) -> (int32 (B,) exponents e, fp16 x * 2^-e in x's layout).
+    e = frexp(max |x[b]|) - t, so the scaled max lies in [2^(t-1), 2^t) (conv.py:49-54)."""
+    _dev_check(x)
+    nd = x.dim() - 2
+    x = _sample_major(x, nd)
+    B = x.shape[0]
+    n = x[0].numel() if B else 0
+    exps = torch.empty((B,), device=x.device, dtype=torch.int32)
+    x16 = torch.empty_like(x, dtype=torch.float16)
+    if B and n:
+        wsb = lib().tbf16_conv_input_ws_bytes(B, n)
+        ws = torch.empty(max(wsb, 16), device=x.device, dtype=torch.uint8)
+        launch("tbf16_conv_input", x, ptr(x), B, n, int(t), ptr(exps), ptr(x16), ptr(ws), ws.numel())
+    return exps, x16
+
+
+def unscale_output(y16: torch.Tensor, exps: torch.Tensor, w_sinv: torch.Tensor, bias=None) -> torch.Tensor:
+    """fp16 (B, O, *spatial) -> bf16 y16 * 2^e[b] * w_sinv[o] + bias[o] (conv.py:56-60)."""
+    nd = y16.dim() - 2
+    y16 = _sample_major(y16, nd)
+    cl = 0 if y16.is_contiguous() else 1
+    B, O = y16.shape[:2]
+    P = y16[0, 0].numel() if B and O else 0
+    out = torch.empty_like(y16, dtype=torch.bfloat16)
+    ws = w_sinv.float().contiguous()
+    b = None if bias is None else bias.detach().float().contiguous()
+    if out.numel():
+        launch("tbf16_conv_epilogue", y16, ptr(y16), B, O, P, cl, ptr(exps), ptr(ws), ptr(b), ptr(out))
+    return out
+
+
+def _scaled_conv_forward(self, x, weight, bias):
+    """Replaces _ConvNd._conv_forward (conv.py:34-60). `weight` is the removed bf16
+    parameter (None); the fp16 copy lives in weight16."""
+    if x.dtype != torch.bfloat16 or (torch.is_grad_enabled() and x.requires_grad):
+        bias = None if bias is None else bias.to(x.dtype)
+        return self._native_conv_forward(x, self.dequantized_weight().to(x.dtype), bias)
+    nd = self.weight16.dim() - 2
+    if x.dim() == nd + 1:  # unbatched input: one sample
+        return _scaled_conv_forward(self, x.unsqueeze(0), weight, bias).squeeze(0)
+    O = self.out_channels
+    if self._tbf16_pointwise:
+        return scaled_linear(x.movedim(1, -1), self.weight16.view(O, -1), self.weight_scale, bias).movedim(-1, 1)
+    if self.padding_mode != "zeros":
+        x = F.pad(x, self._reversed_padding_repeated_twice, mode=self.padding_mode)
+        padding = 0
+    else:
+        padding = self.padding
+    exps, x16 = scale_input(x, self._tbf16_target_exp)
+    y16 = _CONV[nd](x16, self.weight16, None, self.stride, padding, self.dilation, self.groups)
+    return unscale_output(y16, exps, self.weight_scale, bias)
+
+
+def _dequantized_weight(self):
+    w = self.weight16.float() * self.weight_scale.view((-1,) + (1,) * (self.weight16.dim() - 1))
+    return w.bfloat16()
+
+
+_classes = {}
+
+
+def _scaled_class(cls):
+    """A subclass of cls whose _conv_forward is the scaled one, so subclass forwards
+    that end in super().forward keep working (conv.py:71-78)."""
+    if cls not in _classes:
+        _classes[cls] = type(f"TBF16{cls.__name__}", (cls,), {
+            "_native_conv_forward": cls._conv_forward,
+            "_conv_forward": _scaled_conv_forward,
+            "dequantized_weight": _dequantized_weight,
+        })
+    return _classes[cls]
+
+
+def convertible(m: nn.Module) -> bool:
+    """A bf16 nn.Conv1d/2d/3d (or subclass) on the GPU, not converted yet (conv.py:81-83)."""
+    return (isinstance(m, (nn.Conv1d, nn.Conv2d, nn.Conv3d)) and type(m) not in _classes.values()
+            and isinstance(m.weight, torch.Tensor) and m.weight.dtype == torch.bfloat16 and m.weight.is_cuda)
+
+
+def convert_conv(conv: nn.Module):
+    """Convert one bf16 nn.Conv{1,2,3}d (or subclass) in place (conv.py:86-103).
+    `.weight` becomes None; the buffers weight16 (fp16, the weight's shape) and
+    weight_scale (fp32 per output channel) replace it; use .dequantized_weight()."""
+    w = conv.weight.data
+    O = w.shape[0]
+    K = w[0].numel()
+    t = _target_exp(K)
+    w16, ws = prepare_weight(w.reshape(O, K))
+    del conv._parameters["weight"]
+    conv.register_parameter("weight", None)
+    conv.register_buffer("weight16", w16.contiguous().view(w.shape))
+    conv.register_buffer("weight_scale", ws)
+    conv._tbf16_target_exp = t
+    no_pad = conv.padding == "valid" or not isinstance(conv.padding, str) and all(p == 0 for p in conv.padding)
+    conv._tbf16_pointwise = (all(k == 1 for k in conv.kernel_size) and all(s == 1 for s in conv.stride) and no_pad
+                             and conv.groups == 1)
+    conv.__class__ = _scaled_class(type(conv))
+    return conv

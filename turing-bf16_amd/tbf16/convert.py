@@ -9,8 +9,8 @@ one exact power-of-two scale per output row (same memory as bf16, same values).
 Training: every nn.Linear becomes a tbf16.TrainLinear (an nn.Linear subclass, same
 parameters) whose forward and backward run on fp16 MFMA for bf16 inputs.
 Both route F.scaled_dot_product_attention to tbf16's scaled attention for bf16 inputs.
-Convolutions are left native on MI355X (the reference's conv path is not part of
-this build; `conv` is accepted for signature compatibility).
+With conv=True (inference) every bf16 Conv1d/2d/3d becomes a scaled fp16 convolution
+(tbf16.conv).
 """
 import os
 import warnings
@@ -21,6 +21,7 @@ import torch.nn.functional as F
 
 from . import autograd
 from .attention import sdpa
+from .conv import convert_conv, convertible
 from .ops import prepare_weight, scaled_linear
 
 # Train mode: linear layers with in or out features below this run in fp32 (tbf16/convert.py:26-27).
@@ -144,6 +145,8 @@ def convert(model, train: bool = False, sdpa: bool = True, force: bool = False, 
                     and owners[id(child.weight)] == 1):
                 setattr(mod, cname, Linear(child))
                 child.weight = None  # free the bf16 copy now, not when convert() returns
+            elif conv and convertible(child) and owners[id(child.weight)] == 1:
+                convert_conv(child)
     if torch.cuda.is_available():
         torch.cuda.empty_cache()
     if sdpa:
