@@ -6,8 +6,9 @@
 //   clamped to [ek - 14, 14 - eq], ev[b, hkv] = frexp(amax v[b, hkv]) - v_exp.
 // A conversion pass (whose blocks also derive a and ev from those maxima) writes
 // k16 = k * 2^-a and v16 = v * 2^-ev (exact powers of two) to the workspace as
-// fp16, k16 row-major (B, Hkv, Skp, DP) and v16 transposed (B, Hkv, DP, Skp) with
-// keys permuted as the PV operand wants them, both zero-padded, so the forward
+// fp16, k16 row-major (B, Hkv, Skp, DP) and v16 transposed per 64-key tile
+// (B, Hkv, Skp / 64, DP, 64: each tile's V^T one contiguous 2 * 64 * DP-byte
+// block) with keys permuted as the PV operand wants them, both zero-padded, so the forward
 // kernel copies K and V tiles global -> LDS directly (buffer_load ... lds, no
 // registers in between): each K/V element is converted once instead of once per
 // query block. q16 = q * 2^a is converted on the fly (once per
@@ -52,7 +53,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 struct FwdParams {
   const uint16_t *q, *k, *v;
-  uint16_t *k16, *vt16;  // workspace copies: (B, Hkv, Skp, DP) and (B, Hkv, DP, Skp)
+  uint16_t *k16, *vt16;  // workspace copies: (B, Hkv, Skp, DP) and (B, Hkv, Skp / BKV, DP, BKV)
   int32_t* ex;           // workspace exponents {a, 0, ev[b * Hkv + hk]...}
   int Skp, DPc;
   int64_t q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss;
@@ -154,18 +155,45 @@ __device__ __forceinline__ void heads_max(const float* part, int nbh, int nch, F
 // (row c / (DP / 8), chunk c % (DP / 8)). V: thread t takes blocks t + 256 i of 4
 // keys x 8 columns (kg = block % 16, dc = block / 16), converts the four 16-byte
 // row pieces and writes, for each of its 8 columns d, the 4-key run at position
-// perm16(4 kg) of row d (8 bytes; the 16 threads of one dc fill each row segment).
-// Keys past Sk and columns past D are written as zeros.
-// Each block first derives the exponents (tbf16/attention.py:267-277) from the
+// perm16(4 kg) of row d of the tile's V^T block (8 bytes; the 16 threads of one dc
+// fill each 128-byte row; the tile's DP rows are one contiguous block, which the
+// forward kernel then copies to LDS 1 KB at a time). Keys past Sk and columns
+// past D are written as zeros.
+// Each block also derives the exponents (tbf16/attention.py:267-277) from the
 // per-head partial maxima: a from all q and k heads, ev of its own kv head;
 // blocks (0, bhk) store them (a by block (0, 0)) to the workspace and to the
 // caller's exps, where the forward kernel and the backward read them.
 template <int DP>
 __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
   constexpr int CPR = DP / 8;
+  constexpr int NKL = BKV * CPR / 256;         // K chunks per thread
+  constexpr int NVB = (16 * CPR + 255) / 256;  // V blocks of 4 keys x 8 columns per thread
   __shared__ int red[4];
   const int bhk = blockIdx.y, b = bhk / p.Hkv, hk = bhk % p.Hkv;
   const int key0 = blockIdx.x * BKV;
+  const uint16_t* kb = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+  const uint16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
+  // The raw tiles are loaded first (they do not depend on the exponents), so they
+  // are in flight together with the partial-maxima loads of the exponent
+  // derivation below; its first block barrier waits for both.
+  uint4 kr[NKL], vr[NVB][4];
+#pragma unroll
+  for (int i = 0; i < NKL; ++i) {
+    const int c = threadIdx.x + i * 256, row = c / CPR, ch = c % CPR;
+    const int key = key0 + row;
+    kr[i] = key < p.Sk && ch * 8 < p.D ? ldg16(kb + (int64_t)key * p.k_ss + ch * 8) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < NVB; ++i) {
+    const int blk = threadIdx.x + i * 256;
+    const int kg = blk & 15, dc = blk >> 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = key0 + 4 * kg + r;
+      vr[i][r] = blk < 16 * CPR && key < p.Sk && dc * 8 < p.D ? ldg16(vb + (int64_t)key * p.v_ss + dc * 8)
+                                                              : make_uint4(0, 0, 0, 0);
+    }
+  }
   int eq = INT_MIN, ek = INT_MIN;
   heads_max(p.part_q, p.B * p.H, p.nch_q, [&](int, float m) { eq = max(eq, frexp_exp(m)); });
   heads_max(p.part_k, p.B * p.Hkv, p.nch_k, [&](int, float m) { ek = max(ek, frexp_exp(m)); });
@@ -193,30 +221,21 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
     }
   }
   const float sk = ldexp1(-a), sv = ldexp1(-ev);
-  const uint16_t* kb = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
-  const uint16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)hk * p.v_sh;
   uint16_t* k16 = p.k16 + ((int64_t)bhk * p.Skp + key0) * DP;
-  uint16_t* vt16 = p.vt16 + (int64_t)bhk * DP * p.Skp + key0;
+  uint16_t* vt16 = p.vt16 + ((int64_t)bhk * p.Skp + key0) * DP;  // this tile's (DP, BKV) block
 #pragma unroll
-  for (int i = 0; i < BKV * CPR / 256; ++i) {
+  for (int i = 0; i < NKL; ++i) {
     const int c = threadIdx.x + i * 256, row = c / CPR, ch = c % CPR;
-    const int key = key0 + row;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (key < p.Sk && ch * 8 < p.D) v = cvt_bf16x8_f16x8(ldg16(kb + (int64_t)key * p.k_ss + ch * 8), sk);
-    stg16(k16 + row * DP + ch * 8, v);
+    stg16(k16 + row * DP + ch * 8, cvt_bf16x8_f16x8(kr[i], sk));
   }
 #pragma unroll
-  for (int i = 0; i < (16 * CPR + 255) / 256; ++i) {
+  for (int i = 0; i < NVB; ++i) {
     const int blk = threadIdx.x + i * 256;
     if (blk >= 16 * CPR) break;
     const int kg = blk & 15, dc = blk >> 4;
     uint4 cv[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = key0 + 4 * kg + r;
-      cv[r] = make_uint4(0, 0, 0, 0);
-      if (key < p.Sk && dc * 8 < p.D) cv[r] = cvt_bf16x8_f16x8(ldg16(vb + (int64_t)key * p.v_ss + dc * 8), sv);
-    }
+    for (int r = 0; r < 4; ++r) cv[r] = cvt_bf16x8_f16x8(vr[i][r], sv);
     const int pos = perm16(4 * kg);
     const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&cv[0]);
     const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&cv[1]);
@@ -224,7 +243,7 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
     const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&cv[3]);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<uint2*>(vt16 + (int64_t)(dc * 8 + j) * p.Skp + pos) =
+      *reinterpret_cast<uint2*>(vt16 + (dc * 8 + j) * BKV + pos) =
           gather4(w0[j >> 1], w1[j >> 1], w2[j >> 1], w3[j >> 1], j & 1);
   }
 }
@@ -310,7 +329,7 @@ attn_fwd_kernel(FwdParams p) {
       } else {
         const int byte = (bi - KBLK) * 1024 + 16 * lane, d = byte >> 7, phys = (byte & 127) >> 4;
         const int ch = (swz_vt(d, phys) - d * 128) >> 4;
-        voff[i] = (d * p.Skp + ch * 8) * 2;
+        voff[i] = (d * BKV + ch * 8) * 2;
       }
     }
     auto dload = [&](uint8_t* stage, int kb) {
@@ -319,7 +338,7 @@ attn_fwd_kernel(FwdParams p) {
       for (int i = 0; i < BPW; ++i) {
         const uint32_t dst = base + (wave + NW * i) * 1024;
         if (i < KPW) buf_load16_lds(kres, dst, voff[i], kb * BKV * DP * 2);
-        else buf_load16_lds(vres, dst, voff[i], kb * BKV * 2);
+        else buf_load16_lds(vres, dst, voff[i], kb * BKV * DP * 2);
       }
     };
 
@@ -555,7 +574,7 @@ struct WsLayout {
 };
 
 // partial maxima of q | k | v, exponents {a, 0, ev...}, k16 (B, Hkv, Skp, DP),
-// v16^T (B, Hkv, DP, Skp); Skp = Sk rounded up to the 64-key tile
+// v16^T per key tile (B, Hkv, Skp / 64, DP, 64); Skp = Sk rounded up to the 64-key tile
 WsLayout fwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
   WsLayout w;
   w.nch_q = head_amax_chunks(B * H, Sq);
