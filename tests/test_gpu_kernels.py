@@ -103,15 +103,20 @@ GEMM_CFG_M = {0: 300, 1: 300, 2: 300, 3: 300, 4: 300, 5: 29, 6: 29, 7: 61, 8: 61
               13: 29}
 
 
+@pytest.mark.parametrize("K", [200, 1000, 3040])
 @pytest.mark.parametrize("cfg", sorted(GEMM_CFG_M))
-def test_gemm_small_integers_bit_exact(dev, cfg):
-    """Entries in {-1, 0, 1}, K = 200: every partial sum is an integer below 256, so
-    the fp32 accumulation and the bf16 output are exact and the result must equal
-    the integer product bit for bit. Ragged M, N, K exercise every tile edge (and,
-    for the skinny kernel, a K chunk that runs past K); pow2 scales and an integer
-    bias exercise the epilogue."""
+def test_gemm_small_integers_bit_exact(dev, cfg, K):
+    """Entries in {-1, 0, 1}: every partial sum is an integer of at most K, so the
+    fp32 accumulation is exact and the bf16 output must equal the integer product
+    rounded once, bit for bit. Ragged M, N, K exercise every tile edge (and, for
+    the skinny kernel, a K chunk that runs past K); K = 1000 (16 k tiles) and
+    K = 3040 (48 chunks of 64, the last one partial) also run the steady-state
+    loops, whose register sets must never carry the partial last chunk unmasked
+    (K = 3040 puts it right at the steady-state bound of every skinny depth);
+    K = 200 runs only the tails; pow2 scales and an integer bias exercise the
+    epilogue."""
     g = torch.Generator().manual_seed(3)
-    M, N, K = GEMM_CFG_M[cfg], 264, 200
+    M, N = GEMM_CFG_M[cfg], 264
     a = torch.randint(-1, 2, (M, K), generator=g)
     b = torch.randint(-1, 2, (N, K), generator=g)
     bias = torch.randint(-8, 9, (N,), generator=g)
@@ -130,7 +135,7 @@ def test_gemm_small_integers_bit_exact(dev, cfg):
     ones = torch.ones(N, device=dev)
     _ext.call("tbf16_linear", xb.data_ptr(), M, K, K, b16.data_ptr(), N, K, ones.data_ptr(), None, y.data_ptr(), N, 15,
               0, cfg, e.data_ptr(), _ext.stream())
-    assert torch.equal(y.cpu(), (a @ b.t()).bfloat16())
+    assert torch.equal(y.cpu(), (a @ b.t()).double().bfloat16())
 
 
 def test_gemv_small_integers_bit_exact(dev):

@@ -606,8 +606,10 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
   // Steady state: unconditional loads, and scheduling barriers between the
   // steps so that the compiler keeps each step's loads after its MFMAs (left
   // free, it hoists the next chunks' loads, reuses their registers early and
-  // ends up waiting for loads it has just issued).
-  for (; i0 + 2 * PF - 1 < NI; i0 += PF) {
+  // ends up waiting for loads it has just issued). It loads chunks up to
+  // i0 + 2 PF - 1 and stops before reaching the wave's last chunk NI - 1, the
+  // only one that can run past K: that one is always loaded masked, below.
+  for (; i0 + 2 * PF < NI; i0 += PF) {
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
       compute(wr[u], xr[u]);
@@ -679,7 +681,8 @@ struct TileCfg {
 // Two-stage k 64 loop with the last k step deferred past the barrier:
 // 9: 256x256, 8 waves of 64x128, 1 set
 // 10: 256x128, 8 waves of 64x64, 1 set
-// 11: 256x64, 8 waves of 64x32, 2 sets
+// 11: 256x64, 8 waves of 64x32, 3 sets (a k tile is only ~512 MFMA cycles here:
+//     3 sets in flight 31.8 -> 30.2 us at M = 255, N = 10240, K = 2560; 4 or 6 slower)
 // and 12: 128x64, 4 waves of 64x32, k 64, 3 sets, 3 stages
 // Skinny, M <= 32: 13: 64 b rows per block, 8 waves splitting K, 3 chunks in flight
 constexpr TileCfg kCfgs[] = {{256, 256, 32}, {128, 128, 64}, {64, 64, 64},       {128, 128, 64},    {256, 256, 32},
@@ -755,7 +758,7 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
     case 4: CFG(256, 256, 4, 2, 32, 3, 2); break;
     case 9: CFG(256, 256, 4, 2, 64, 1, 5); break;
     case 10: CFG(256, 128, 4, 2, 64, 1, 5); break;
-    case 11: CFG(256, 64, 4, 2, 64, 2, 5); break;
+    case 11: CFG(256, 64, 4, 2, 64, 3, 5); break;
     case 12: CFG(128, 64, 2, 2, 64, 3, 3); break;
 #define SKINNY(NB_, MB_, NW_, PF_, TR_)                                                                         \
   skinny_kernel<NB_, MB_, NW_, PF_, TR_, A_BF16><<<g, NW_ * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, \
