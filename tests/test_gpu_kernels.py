@@ -194,6 +194,37 @@ def test_cfg3_small_m(dev, M):
     _linear_checks(xs[M], w, dev, f"cfg3 M={M}")
 
 
+@pytest.mark.parametrize("cfg", [-1, 5, 6, 7, 13])
+@pytest.mark.parametrize("l1", [0, 1])
+def test_skinny_row_exponents_and_output(dev, cfg, l1):
+    """Decode-sized tbf16_linear on the skinny configurations: the row exponents it
+    leaves in the caller's workspace equal the oracle's bit for bit (max and L1
+    rows, K not a multiple of 64, rows spanning 2^-30 .. 2^30, a zero row), and the
+    output equals the same kernel run on those exponents (tbf16_linear_exps)."""
+    g = torch.Generator().manual_seed(7 + l1)
+    M = 29 if cfg in (-1, 5, 6, 13) else 61
+    N, K = 10240 if cfg == -1 else 264, 2504
+    x = (torch.randn(M, K, generator=g) * torch.ldexp(torch.ones(M, 1), torch.randint(-30, 31, (M, 1), generator=g))
+         ).bfloat16()
+    x[3] = 0.0
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    xd, wd = x.to(dev), w.to(dev)
+    w16, ws = ops.prepare_weight(wd)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    e = torch.full((M,), -999, dtype=torch.int32, device=dev)
+    _ext.call("tbf16_linear", xd.data_ptr(), M, K, K, w16.data_ptr(), N, K, ws.data_ptr(), None, y.data_ptr(), N, 15,
+              l1, cfg, e.data_ptr(), _ext.stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(e.cpu().numpy(), O.row_exps(x, 15, bool(l1)))
+    c = cfg if cfg >= 0 else 13
+    y2 = torch.empty_like(y)
+    _ext.call("tbf16_linear_exps", xd.data_ptr(), M, K, K, e.data_ptr(), w16.data_ptr(), N, K, ws.data_ptr(), None,
+              y2.data_ptr(), N, c, _ext.stream())
+    assert torch.equal(y, y2)
+    ref = (x.double() @ (w16.cpu().double() * ws.cpu().double()[:, None]).t())
+    assert rel(y.cpu(), ref) < TOL
+
+
 # ---- Config 4: scaled attention forward ------------------------------------------
 
 def _attn_checks(q, k, v, dev, rows=None, label=""):
