@@ -275,6 +275,37 @@ def test_autograd_sdpa(dev, name, Hq, Hkv, S, D, causal, qs, gs, vs):
         assert torch.isfinite(o).all() and e < 3e-3, (name, n, e)
 
 
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [(6, 2, 300, 520, 112, True), (4, 4, 520, 300, 64, True),
+                                                   (4, 4, 200, 333, 128, False), (2, 2, 130, 70, 256, True)])
+def test_autograd_sdpa_ragged(dev, Hq, Hkv, Sq, Sk, D, causal):
+    """Query and key lengths that differ and are multiples of no tile, head dim 112
+    (zero-padded to 128) through the backward, GQA: causal is top-left aligned as
+    torch's is_causal (key j visible to query i iff j <= i; with Sq > Sk the last
+    rows see every key). Output and gradients against fp64."""
+    q = randn(1, Hq, Sq, D, seed=60).bfloat16().to(dev)
+    k = randn(1, Hkv, Sk, D, seed=61).bfloat16().to(dev)
+    v = randn(1, Hkv, Sk, D, seed=62).bfloat16().to(dev)
+    do = randn(1, Hq, Sq, D, seed=63).bfloat16().to(dev)
+    keep = torch.ones(Sq, Sk, dtype=torch.bool, device=dev).tril()
+
+    def ref(q, k, v):
+        k, v = k.repeat_interleave(Hq // Hkv, 1), v.repeat_interleave(Hq // Hkv, 1)
+        s = q @ k.transpose(-1, -2) / math.sqrt(D)
+        if causal:
+            s = s.masked_fill(~keep, float("-inf"))
+        return torch.softmax(s, -1) @ v
+
+    r = _grads(ref, [q.double(), k.double(), v.double()], do.double())
+    ours = _grads(lambda q, k, v: ag.sdpa(q, k, v, is_causal=causal, enable_gqa=Hq != Hkv), [q, k, v], do)
+    for n, o, rr in zip(["o", "dq", "dk", "dv"], ours, r):
+        e = rel(o, rr)
+        print(f"ragged Sq={Sq} Sk={Sk} D={D} {n}: {e:.3e}")
+        assert o.shape == rr.shape and torch.isfinite(o).all() and e < 3e-3, (n, e)
+    with torch.no_grad():
+        e = rel(tbf16.sdpa(q, k, v, is_causal=causal, enable_gqa=Hq != Hkv), r[0])
+    assert e < 3e-3, e
+
+
 @pytest.mark.parametrize("causal,D,Hq,Hkv,S", [(False, 64, 4, 4, 384), (True, 128, 8, 4, 520), (True, 256, 2, 2, 300)])
 def test_sdpa_dropout(dev, causal, D, Hq, Hkv, S):
     """Dropout in the fused kernels against an fp64 reference that applies the
