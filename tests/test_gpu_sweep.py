@@ -86,3 +86,62 @@ def _causal64(q, k, v):
             s = (q[b, h].double() @ k[b, hk].double().t()) / math.sqrt(D)
             out[b, h] = torch.softmax(s.masked_fill(~keep, float("-inf")), -1) @ v[b, hk].double()
     return out
+
+
+_R2 = random.Random(20261202)
+BWD_SHAPES = []
+for _ in range(8):
+    hkv = _R2.choice([1, 2])
+    BWD_SHAPES.append((_R2.choice([1, 2]), hkv * _R2.choice([1, 2, 3]), hkv, _R2.randint(16, 600), _R2.randint(16, 600),
+                       8 * _R2.randint(1, 32), _R2.random() < 0.5))
+TRAIN_LINEAR_SHAPES = [(_R2.randint(2, 700), 8 * _R2.randint(1, 100), 8 * _R2.randint(1, 100)) for _ in range(6)]
+
+
+def _grads(fn, inputs, dout):
+    ins = [t.detach().clone().requires_grad_() for t in inputs]
+    out = fn(*ins)
+    out.backward(dout)
+    return [out] + [t.grad for t in ins]
+
+
+@pytest.mark.parametrize("B,H,Hkv,Sq,Sk,D,causal", BWD_SHAPES,
+                         ids=[f"{b}x{h}/{hk}x{sq}x{sk}xD{d}{'c' if c else ''}" for b, h, hk, sq, sk, d, c in BWD_SHAPES])
+def test_attention_backward_sweep(dev, B, H, Hkv, Sq, Sk, D, causal):
+    """tbf16.autograd.sdpa forward and backward (dq, dk, dv with the GQA group sums)
+    against fp64 autograd on the same bf16 inputs."""
+    import tbf16.autograd as ag
+    g = torch.Generator().manual_seed(B * 997 + H * 89 + Sq * 5 + Sk * 11 + D)
+    q = torch.randn(B, H, Sq, D, generator=g).bfloat16().to(dev)
+    k = torch.randn(B, Hkv, Sk, D, generator=g).bfloat16().to(dev)
+    v = torch.randn(B, Hkv, Sk, D, generator=g).bfloat16().to(dev)
+    do = torch.randn(B, H, Sq, D, generator=g).bfloat16().to(dev)
+    keep = torch.ones(Sq, Sk, dtype=torch.bool, device=dev).tril()
+
+    def ref(q, k, v):
+        k, v = k.repeat_interleave(H // Hkv, 1), v.repeat_interleave(H // Hkv, 1)
+        s = q @ k.transpose(-1, -2) / math.sqrt(D)
+        if causal:
+            s = s.masked_fill(~keep, float("-inf"))
+        return torch.softmax(s, -1) @ v
+
+    r = _grads(ref, [q.double(), k.double(), v.double()], do.double())
+    ours = _grads(lambda q, k, v: ag.sdpa(q, k, v, is_causal=causal, enable_gqa=H != Hkv), [q, k, v], do)
+    for n, o, rr in zip(["o", "dq", "dk", "dv"], ours, r):
+        e = rel(o, rr)
+        assert o.shape == rr.shape and torch.isfinite(o).all() and e < 3e-3, (n, e)
+
+
+@pytest.mark.parametrize("M,K,N", TRAIN_LINEAR_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in TRAIN_LINEAR_SHAPES])
+def test_train_linear_sweep(dev, M, K, N):
+    """tbf16.autograd.linear with bias: y, dx, dw, db against fp64 autograd."""
+    import tbf16.autograd as ag
+    g = torch.Generator().manual_seed(M * 13 + K * 7 + N)
+    x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).bfloat16().to(dev)
+    b = torch.randn(N, generator=g).bfloat16().to(dev)
+    dy = (torch.randn(M, N, generator=g) * 1e-3).bfloat16().to(dev)
+    r = _grads(lambda x, w, b: x @ w.t() + b, [x.double(), w.double(), b.double()], dy.double())
+    ours = _grads(lambda x, w, b: ag.linear(x, w, b), [x, w, b], dy)
+    for n, o, rr in zip(["y", "dx", "dw", "db"], ours, r):
+        e = rel(o, rr)
+        assert o.shape == rr.shape and torch.isfinite(o).all() and e < 3e-3, (n, e)
