@@ -254,3 +254,10 @@ def test_conv_native_paths_and_unbatched(dev):
     assert y1.shape == (12, 9, 9) and O.rel_err(y1.cpu(), y2[1].cpu()) < 1e-3
     with torch.no_grad():
         assert tc(x[:0]).shape == (0, 12, 9, 9)
+    # helpers reject the wrong dtypes; samples with no elements take amax = 1
+    with pytest.raises(TypeError):
+        tconv.scale_input(x.half(), 0)
+    e, x16 = tconv.scale_input(torch.empty(3, 0, 4, 4, dtype=torch.bfloat16, device=dev), -2)
+    assert e.tolist() == [3, 3, 3] and x16.shape == (3, 0, 4, 4)
+    with pytest.raises(TypeError):
+        tconv.unscale_output(x, e, tc.weight_scale)

@@ -37,8 +37,11 @@ def _sample_major(x: torch.Tensor, nd: int) -> torch.Tensor:
 
 def scale_input(x: torch.Tensor, t: int):
     """bf16 (B, C, *spatial) -> (int32 (B,) exponents e, fp16 x * 2^-e in x's layout).
-    e = frexp(max |x[b]|) - t, so the scaled max lies in [2^(t-1), 2^t) (conv.py:49-54)."""
+    e = frexp(max |x[b]|) - t, so the scaled max lies in [2^(t-1), 2^t) (conv.py:49-54).
+    Empty samples take amax = 1 as the reference's where(amax > 0, amax, 1) does."""
     _dev_check(x)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"tbf16.conv.scale_input: expected bf16, got {x.dtype}")
     nd = x.dim() - 2
     x = _sample_major(x, nd)
     B = x.shape[0]
@@ -49,11 +52,17 @@ def scale_input(x: torch.Tensor, t: int):
         wsb = lib().tbf16_conv_input_ws_bytes(B, n)
         ws = torch.empty(max(wsb, 16), device=x.device, dtype=torch.uint8)
         launch("tbf16_conv_input", x, ptr(x), B, n, int(t), ptr(exps), ptr(x16), ptr(ws), ws.numel())
+    elif B:
+        exps.fill_(1 - int(t))
     return exps, x16
 
 
 def unscale_output(y16: torch.Tensor, exps: torch.Tensor, w_sinv: torch.Tensor, bias=None) -> torch.Tensor:
     """fp16 (B, O, *spatial) -> bf16 y16 * 2^e[b] * w_sinv[o] + bias[o] (conv.py:56-60)."""
+    _dev_check(y16, exps, w_sinv)
+    if y16.dtype != torch.float16 or exps.dtype != torch.int32 or exps.numel() != y16.shape[0]:
+        raise TypeError("tbf16.conv.unscale_output: expected fp16 y16 and int32 exponents, one per sample")
+    exps = exps.contiguous()
     nd = y16.dim() - 2
     y16 = _sample_major(y16, nd)
     cl = 0 if y16.is_contiguous() else 1
