@@ -112,3 +112,22 @@ def test_public_api_names():
         assert hasattr(tbf16.ops, n)
     for n in ["head_exp", "head_scale", "prepare_qkv", "expand_heads"]:
         assert hasattr(tbf16.attention, n)
+
+
+def test_conv_module_host_logic():
+    """tbf16.conv without a GPU: the public names of conv.py, convertible() only for
+    bf16 GPU convs not yet converted, the generated TBF16<Conv> subclass keeps the
+    native _conv_forward for the fallback path and is made once per class, and
+    convert(force=True) leaves CPU convs alone."""
+    from tbf16 import conv as tconv
+    for n in ["convert_conv", "convertible", "scale_input", "unscale_output"]:
+        assert hasattr(tconv, n)
+    c2 = nn.Conv2d(4, 8, 3).bfloat16()
+    assert not tconv.convertible(c2)  # on the CPU
+    assert not tconv.convertible(nn.Linear(4, 4))
+    cls = tconv._scaled_class(nn.Conv2d)
+    assert cls.__name__ == "TBF16Conv2d" and issubclass(cls, nn.Conv2d)
+    assert cls._native_conv_forward is nn.Conv2d._conv_forward and tconv._scaled_class(nn.Conv2d) is cls
+    m = nn.Sequential(nn.Conv2d(4, 8, 3).bfloat16(), nn.Conv1d(4, 4, 1).bfloat16())
+    tbf16.convert(m, sdpa=False, force=True)
+    assert type(m[0]) is nn.Conv2d and type(m[1]) is nn.Conv1d and m[0].weight is not None
