@@ -2,7 +2,8 @@
 
 Sources (reference tree): tests/test_ops.py (asserts < 3e-3, finite),
 tests/test_outliers.py (<= 1.5x torch bf16's small-channel error),
-tests/test_sdpa_api.py (< 1e-2, bf16, finite; patch() stats),
+tests/test_sdpa_api.py (< 1e-2, bf16, finite; patch() stats), tests/test_attention.py
+(print-only there; its scaled cases asserted here at 3e-3),
 tests/test_accuracy.py, tests/test_small_m.py, tests/test_autograd.py (print-only
 there; asserted here with the same 3e-3 bar) and tbf16/__main__.py (< 3e-3).
 Inputs come from seeded CPU generators (the reference's CUDA-RNG values are not
@@ -273,6 +274,26 @@ def test_autograd_sdpa(dev, name, Hq, Hkv, S, D, causal, qs, gs, vs):
         e = rel(o, r)
         print(f"{name} {n}: {e:.3e}")
         assert torch.isfinite(o).all() and e < 3e-3, (name, n, e)
+
+
+ATTN_SCALE_CASES = {"gaussian": (1, 1, 1), "q,k x30 (peaky softmax)": (30, 30, 1), "v x1e5": (1, 1, 1e5),
+                    "v x1e-7": (1, 1, 1e-7), "q x1e3, k x1e-3": (1e3, 1e-3, 1), "q,k x300, v x1e6": (300, 300, 1e6)}
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("name", list(ATTN_SCALE_CASES))
+def test_reference_attention_scale_cases(dev, name, causal):
+    """tests/test_attention.py:20-38 of the reference (print-only there): the same
+    scaled inputs at (1, 8, 2048, 128), asserted here at 3e-3 against fp64."""
+    a, b, c = ATTN_SCALE_CASES[name]
+    q, k, v = (randn(1, 8, 2048, 128, seed=80 + i).bfloat16().to(dev) for i in range(3))
+    q, k, v = q * a, k * b, v * c
+    r = _ref_sdpa(q.double(), k.double(), v.double(), causal)
+    with torch.no_grad():
+        o = tbf16.sdpa(q, k, v, is_causal=causal)
+    e = rel(o, r)
+    print(f"{'causal ' if causal else ''}{name}: tbf16 {e:.2e}")
+    assert torch.isfinite(o).all() and e < 3e-3, e
 
 
 @pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [(6, 2, 300, 520, 112, True), (4, 4, 520, 300, 64, True),
