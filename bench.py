@@ -294,16 +294,18 @@ def profile_run(what: str):
         x, w, _ = W.cfg2_square_gemm()
         x, w = x.to(dev), w.to(dev)
         w16, ws = tbf16.prepare_weight(w)
-        for _ in range(5):
+        for _ in range(40):
             tbf16.scaled_linear(x, w16, ws)
         a = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)  # 256 MiB
         b = torch.empty_like(a)
         for _ in range(5):
             b.copy_(a)
     elif what == "attention":
-        for S in (4096, 16384):
+        # warmed, back-to-back calls as in the bench line (the first calls of a
+        # process run at lower clocks)
+        for S, n in ((4096, 60), (16384, 20)):
             q, k, v = (t.to(dev) for t in W.cfg4_attention(S))
-            for _ in range(3):
+            for _ in range(n):
                 tbf16.sdpa(q, k, v, is_causal=True)
     elif what == "train":
         bench_train(2)

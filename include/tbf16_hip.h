@@ -49,7 +49,7 @@ int tbf16_row_exps(const void* x, int64_t M, int64_t K, int64_t ldx, int t, int 
 
 /* y16 = fp16(x * 2^p[r]) and s_inv[r] = 2^-p[r].
  * Replaces quantize_rows (tbf16/csrc/small_kernels.cu:275-287, kernel :35-74;
- * Python tbf16/ops.py:85-100). */
+ * Python tbf16/ops.py:74-89). */
 int tbf16_quantize_rows(const void* x, int64_t R, int64_t K, int64_t ldx, int t, int l1, void* y16, int64_t ldy,
                         float* s_inv, void* stream);
 
@@ -75,7 +75,7 @@ int tbf16_quantize_cols_t(const void* x, int64_t R, int64_t K, int64_t ldx, int 
  * x bf16 (M, K); w16 fp16 (N, K); ws fp32 (N,); bias bf16 (N,) or NULL; y bf16
  * (M, N). cfg < 0 picks the tile shape. Replaces linear (tbf16/csrc/gemm_sm75.cu:
  * 257-284) and, at 2 <= M < 256, quantize_rows + cuBLAS + epilogue
- * (tbf16/ops.py:174-189) without its fp16 intermediate. */
+ * (tbf16/ops.py:163-178) without its fp16 intermediate. */
 int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N, int64_t ldw,
                  const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg, int32_t* exps_ws,
                  void* stream);
@@ -89,7 +89,7 @@ int tbf16_linear_exps(const void* x, int64_t M, int64_t K, int64_t ldx, const in
 
 /* GEMM on already-quantised fp16 operands, both K-contiguous:
  * y = bf16((a16 @ b16^T) * sa[m] * sb[n] + bias[n]) with fp32 accumulation.
- * Replaces the cuBLAS fp16 GEMM + epilogue pair of linear_q (tbf16/ops.py:178-189,
+ * Replaces the cuBLAS fp16 GEMM + epilogue pair of linear_q (tbf16/ops.py:167-178,
  * small_kernels.cu:289-302) and _scaled_mm (tbf16/autograd.py:49-55). */
 int tbf16_gemm_f16(const void* a16, int64_t M, int64_t K, int64_t lda, const float* sa, const void* b16, int64_t N,
                    int64_t ldb, const float* sb, const void* bias, void* y, int64_t ldy, int cfg, void* stream);
@@ -135,7 +135,7 @@ int tbf16_conv_epilogue(const void* y16, int64_t B, int64_t O, int64_t P, int ch
                         const float* ws, const float* bias, void* out, void* stream);
 
 /* Scaled attention forward (flash-style, no S x S buffer).
- * Exponents (tbf16/attention.py:267-277): eq/ek = max over heads of frexp(amax),
+ * Exponents (tbf16/attention.py:38-48): eq/ek = max over heads of frexp(amax),
  * a = clamp(floor((ek - eq) / 2)), ev[b, hkv] = frexp(amax v[b, hkv]) - v_exp.
  * Computes softmax((q 2^a)(k 2^-a)^T * scale + bias) (v 2^-ev) on fp16 MFMA with
  * fp32 online softmax and writes o = bf16(O / l * 2^ev) once.
@@ -153,7 +153,7 @@ int tbf16_conv_epilogue(const void* y16, int64_t B, int64_t O, int64_t P, int ch
  * passes dropout_p to torch's kernel, whose Philox stream differs: masks are not
  * comparable bit for bit.
  * Replaces prepare_qkv + torch's fp16 memory-efficient SDPA + head_scale
- * (tbf16/attention.py:285-294) and _eff_fwd (tbf16/autograd.py:155-164). */
+ * (tbf16/attention.py:56-65) and _eff_fwd (tbf16/autograd.py:155-164). */
 size_t tbf16_attn_fwd_ws_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);
 int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64_t H, int64_t Hkv, int64_t Sq,
                    int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,

@@ -19,7 +19,14 @@ How each function is pinned (checked by tests/test_oracle.py):
   bf16/fp16 rounding          torch CPU RNE casts (library routines) and pow2.c.
   linear_fused / gemv /       fp64 matmul of the same bf16 values (rel err bound),
   linear_cublas_path          exact small-integer cases where fp32 is exact.
-  attn_exponents / head_exp   torch.frexp on amax; brute-force loop over heads.
+  attn_exponents / head_exp   torch.frexp on amax; brute-force loop over heads; a's
+                              floor and both clamps by the invariants they exist for
+                              (balanced scaled maxima, each at most 2^14, the key's
+                              clamp winning when both bind).
+  sdpa_reference_arith /      fp64 softmax attention within fp16-level error; the
+  sdpa_bwd_reference_arith    closed forms (q = 0 -> prefix means, one-hot copy);
+                              fp64 autograd gradients within fp16-level error; every
+                              output rounding they model checked on its own.
   sdpa_ref64 / attn_*         closed forms: q=0 -> prefix mean of V rows, one-hot
                               logits copy a V row; fp64 autograd for gradients.
   attn_bwd_exponents / retry  closed form of autograd.py:175-189 with an injected
@@ -77,14 +84,14 @@ def pow2_exp(amax, t: int) -> np.ndarray:
 def pow2_exp_fused(amax, t: int) -> np.ndarray:
     """Fused GEMM row_scale variant, tbf16/csrc/gemm_sm75.cu:19-23: only the upper
     clamp on the biased scale exponent. Identical to pow2_exp for t >= 2 (the fused
-    path always uses t = 15, tbf16/ops.py:37)."""
+    path always uses t = 15, tbf16/ops.py:26)."""
     e = np.clip(exp_field(amax), 1, 252)
     se = np.minimum(253 + t - e, 254)
     return (se - 127).astype(np.int32)
 
 
 def pow2_exp_triton(amax, t: int) -> np.ndarray:
-    """Triton fallback variant, tbf16/ops.py:50-56,68,77: 2**(126 - e) * 2**t with
+    """Triton fallback variant, tbf16/ops.py:39-45,57,66: 2**(126 - e) * 2**t with
     no clamp of the result. Returned as an exponent that may exceed 127 (the
     reference then holds inf). Kept only to document where the variants differ."""
     e = np.clip(exp_field(amax), 1, 252)
@@ -99,7 +106,7 @@ def frexp_exp(v) -> np.ndarray:
 
 
 def target_exp(K: int) -> int:
-    """tbf16/ops.py:40-43: rows scaled to amax in [2^(t-1), 2^t) keep |C| < K*4^t."""
+    """tbf16/ops.py:29-32: rows scaled to amax in [2^(t-1), 2^t) keep |C| < K*4^t."""
     return min(0, (15 - math.ceil(math.log2(max(K, 1)))) // 2)
 
 
@@ -113,10 +120,10 @@ def attn_do_target(D: int) -> int:
     return 12 - math.ceil(math.log2(D))
 
 
-L1_TARGET = 15            # tbf16/ops.py:141
-FUSED_T = 15              # tbf16/ops.py:37
-FUSED_MIN_M = 256         # tbf16/ops.py:34
-SMALL_M = 2               # tbf16/ops.py:215
+L1_TARGET = 15            # tbf16/ops.py:130
+FUSED_T = 15              # tbf16/ops.py:26
+FUSED_MIN_M = 256         # tbf16/ops.py:23
+SMALL_M = 2               # tbf16/ops.py:204
 
 
 def ldexp1(p) -> np.ndarray:
@@ -170,7 +177,7 @@ def row_exps(x: torch.Tensor, t: int, l1: bool = False, fused: bool = False) -> 
 def quantize_rows(x: torch.Tensor, t: int = 0, l1: bool = False):
     """bf16 (R, K) -> (fp16 (R, K), fp32 s_inv (R,)).
 
-    Restates quantize_rows (tbf16/ops.py:85-100 -> small_kernels.cu:35-74):
+    Restates quantize_rows (tbf16/ops.py:74-89 -> small_kernels.cu:35-74):
     y = fp16_rne(x * s) with s = 2**p from pow2_exp, s_inv = 1 / s.
     """
     p = row_exps(x, t, l1)
@@ -180,7 +187,7 @@ def quantize_rows(x: torch.Tensor, t: int = 0, l1: bool = False):
 
 
 def prepare_weight(w: torch.Tensor):
-    """tbf16/ops.py:151-153: quantize_rows(w, target_exp(K))."""
+    """tbf16/ops.py:140-142: quantize_rows(w, target_exp(K))."""
     return quantize_rows(w.contiguous(), target_exp(w.shape[1]))
 
 
@@ -227,7 +234,7 @@ def linear_fused(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None
 
 
 def linear_cublas_path(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None) -> torch.Tensor:
-    """The reference's 2 <= M < 256 regime (ops.py:174-189): L1 row scales at
+    """The reference's 2 <= M < 256 regime (ops.py:163-178): L1 row scales at
     t = 15, an fp16 C (cuBLAS fp16 output) and then the bf16 epilogue. This double
     rounding is the reference's own error at small M."""
     x16, sx = quantize_rows(x, L1_TARGET, l1=True)
@@ -236,7 +243,7 @@ def linear_cublas_path(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bia
 
 
 def linear_small_m(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None) -> torch.Tensor:
-    """This build's 2 <= M < 256 path: the reference's L1 exponents (ops.py:174)
+    """This build's 2 <= M < 256 path: the reference's L1 exponents (ops.py:163)
     with fp32 accumulation and a single bf16 rounding (no fp16 C)."""
     x16, sx = quantize_rows(x, L1_TARGET, l1=True)
     acc = x16.float() @ w16.float().t()
@@ -254,7 +261,7 @@ def gemv(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None) -> tor
 
 
 def scaled_linear(x: torch.Tensor, w16: torch.Tensor, ws: torch.Tensor, bias=None) -> torch.Tensor:
-    """Dispatcher of tbf16/ops.py:164-175 as this build runs it: M < 2 -> GEMV,
+    """Dispatcher of tbf16/ops.py:153-164 as this build runs it: M < 2 -> GEMV,
     M >= 256 -> fused (max rows, t = 15), else L1 rows at t = 15; all with fp32
     accumulation and one bf16 rounding."""
     shape = x.shape
@@ -324,12 +331,12 @@ def head_amax(x: torch.Tensor) -> torch.Tensor:
 
 
 def head_exp(x: torch.Tensor) -> torch.Tensor:
-    """tbf16/attention.py:253-256: frexp exponent of each head's amax, int32."""
+    """tbf16/attention.py:24-27: frexp exponent of each head's amax, int32."""
     return torch.frexp(head_amax(x))[1].to(torch.int32)
 
 
 def attn_exponents(q, k, v, v_exp: int):
-    """prepare_qkv exponents (attention.py:267-277): a (scalar) and ev (B, Hkv)."""
+    """prepare_qkv exponents (attention.py:38-48): a (scalar) and ev (B, Hkv)."""
     eq = int(head_exp(q).max())
     ek = int(head_exp(k).max())
     a = (ek - eq) // 2
@@ -339,19 +346,19 @@ def attn_exponents(q, k, v, v_exp: int):
 
 
 def head_scale(x: torch.Tensor, e: torch.Tensor, dtype) -> torch.Tensor:
-    """attention.py:259-264: x * 2**e[b, h] cast to dtype (contiguous)."""
+    """attention.py:30-35: x * 2**e[b, h] cast to dtype (contiguous)."""
     e = e.to(torch.int32).expand(x.shape[0], x.shape[1])
     s = torch.ldexp(torch.ones(e.shape), e.float())
     return (x.float() * s[..., None, None]).to(dtype).contiguous()
 
 
 def expand_heads(e: torch.Tensor, n_heads: int) -> torch.Tensor:
-    """attention.py:280-282."""
+    """attention.py:51-53."""
     return e if e.shape[1] == n_heads else e.repeat_interleave(n_heads // e.shape[1], dim=1)
 
 
 def prepare_qkv(q, k, v, v_exp: int = 0):
-    """attention.py:267-277: scaled fp16 copies and the exponents."""
+    """attention.py:38-48: scaled fp16 copies and the exponents."""
     a, ev = attn_exponents(q, k, v, v_exp)
     at = torch.tensor([[a]], dtype=torch.int32)
     q16 = head_scale(q, at, torch.float16)
@@ -390,9 +397,9 @@ def sdpa_ref64(q, k, v, causal=False, scale=None, mask=None, rows=None):
 
 def sdpa_fp16_emulated(q, k, v, causal=False, scale=None, v_exp=13, rows=None):
     """This build's attention arithmetic on the CPU: fp16 copies scaled by
-    2^a, 2^-a, 2^-ev (attention.py:267-277), logits and softmax in fp32, P
+    2^a, 2^-a, 2^-ev (attention.py:38-48), logits and softmax in fp32, P
     rounded to fp16 for P.V, fp32 accumulation, out = bf16(O / l * 2^ev) with one
-    rounding. The reference itself rounds O to fp16 first (attention.py:292-294)."""
+    rounding. The reference itself rounds O to fp16 first (attention.py:63-65)."""
     q16, k16, v16, a, ev = prepare_qkv(q, k, v, v_exp)
     H, Hkv = q.shape[1], k.shape[1]
     k16e = k16.repeat_interleave(H // Hkv, 1) if Hkv != H else k16
@@ -410,6 +417,95 @@ def sdpa_fp16_emulated(q, k, v, causal=False, scale=None, v_exp=13, rows=None):
     o = (p.half().float() @ v16e.float()) / l
     evq = expand_heads(ev, H).float()
     return (o * torch.ldexp(torch.ones_like(evq), evq)[..., None, None]).bfloat16(), a, ev
+
+
+def sdpa_reference_arith(q, k, v, causal=False, scale=None, v_exp=13, rows=None):
+    """The reference's own inference arithmetic (attention.py:56-65), restated so
+    tests can hold this build to "no worse than the reference's error": prepare_qkv's
+    fp16 copies, then what torch's fp16 memory-efficient kernel computes (logits,
+    row max and softmax sums in fp32, P rounded to fp16 for the P.V product with fp32
+    accumulation, O / l rounded to fp16 as its fp16 output), then head_scale of that
+    fp16 output by 2^ev into bf16: two roundings of the output. One softmax over the
+    whole row replaces the kernel's per-tile online rescaling (the same values up to
+    fp32 rounding). Works on any device; per (b, h) to bound memory."""
+    q16, k16, v16, a, ev = prepare_qkv(q.cpu(), k.cpu(), v.cpu(), v_exp)
+    dev = q.device
+    q16, k16, v16 = q16.to(dev), k16.to(dev), v16.to(dev)
+    B, H, Sq, D = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    sc = (1.0 / math.sqrt(D)) if scale is None else scale
+    idx = torch.arange(Sq, device=dev) if rows is None else torch.as_tensor(rows, device=dev)
+    kj = torch.arange(Sk, device=dev)
+    evq = expand_heads(ev, H)
+    out = torch.empty(B, H, len(idx), D, dtype=torch.bfloat16, device=dev)
+    for b in range(B):
+        for h in range(H):
+            hk = h // (H // Hkv)
+            s = (q16[b, h, idx].float() @ k16[b, hk].float().t()) * sc
+            if causal:
+                s = s.masked_fill(kj[None, :] > idx[:, None], float("-inf"))
+            m = s.amax(-1, keepdim=True)
+            p = torch.exp(s - m)
+            l = p.sum(-1, keepdim=True)
+            o16 = ((p.half().float() @ v16[b, hk].float()) / l).half()
+            out[b, h] = (o16.float() * math.ldexp(1.0, int(evq[b, h]))).bfloat16()
+    return out
+
+
+def sdpa_bwd_reference_arith(q, k, v, dout, causal=False, scale=None):
+    """The reference's training attention arithmetic (autograd.py:149-193) for one
+    attempt without overflow, restated on any device: prepare_qkv(v_exp=0) copies;
+    the fp16 forward (as sdpa_reference_arith, O / l rounded to fp16 = out16, its
+    lse kept in fp32); G from attn_bwd_exponents; dO16 = fp16(dout 2^(ev_q + G));
+    then what the memory-efficient fp16 backward computes: P = exp(s - lse) in fp32,
+    rounded to fp16 for dV = P^T dO16; dP = dO16 V16^T and delta = rowsum(dO16 o
+    out16) in fp32; dS = P (dP - delta) rounded to fp16 for dQ = scale dS K16 and
+    dK = scale dS^T Q16; each gradient accumulated in fp32 and rounded to fp16
+    (dq16, dk16, dv16), GQA groups summed in fp32 (autograd.py:141-146), then
+    head_scale by 2^(a-G), 2^(-a-G), 2^(-ev-G) into bf16. Returns
+    (out bf16, dq, dk, dv bf16, (a, ev, e, G))."""
+    dev = q.device
+    B, H, Sq, D = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    q16, k16, v16, a, ev = prepare_qkv(q.cpu(), k.cpu(), v.cpu(), 0)
+    q16, k16, v16 = q16.to(dev), k16.to(dev), v16.to(dev)
+    evq = expand_heads(ev, H)
+    e, t_do, G = attn_bwd_exponents(dout.cpu(), evq, D)
+    sc = (1.0 / math.sqrt(D)) if scale is None else scale
+    qi = torch.arange(Sq, device=dev)
+    kj = torch.arange(Sk, device=dev)
+    out = torch.empty(B, H, Sq, D, dtype=torch.bfloat16, device=dev)
+    dq = torch.empty(B, H, Sq, D, dtype=torch.bfloat16, device=dev)
+    dk32 = torch.zeros(B, Hkv, Sk, D, dtype=torch.float32, device=dev)
+    dv32 = torch.zeros_like(dk32)
+    for b in range(B):
+        for h in range(H):
+            hk = h // (H // Hkv)
+            Q, K, V = q16[b, h].float(), k16[b, hk].float(), v16[b, hk].float()
+            s = (Q @ K.t()) * sc
+            if causal:
+                s = s.masked_fill(kj[None, :] > qi[:, None], float("-inf"))
+            m = s.amax(-1, keepdim=True)
+            p = torch.exp(s - m)
+            l = p.sum(-1, keepdim=True)
+            o16 = ((p.half().float() @ V) / l).half()
+            out[b, h] = (o16.float() * math.ldexp(1.0, int(evq[b, h]))).bfloat16()
+            lse = m + torch.log(l)
+            do16 = (dout[b, h].float() * math.ldexp(1.0, int(evq[b, h]) + G)).half().float()
+            P = torch.exp(s - lse)
+            dv32[b, hk] += (P.half().float().t() @ do16).half().float()
+            dP = do16 @ V.t()
+            delta = (do16 * o16.float()).sum(-1, keepdim=True)
+            dS = (P * (dP - delta)).half().float()
+            dq16 = ((dS @ K) * sc).half()
+            dk32[b, hk] += ((dS.t() @ Q) * sc).half().float()
+            dq[b, h] = (dq16.float() * math.ldexp(1.0, a - G)).bfloat16()
+    # (with Hkv == H each sum holds one fp16 value, which head_scale scales directly)
+    sv = torch.tensor([[math.ldexp(1.0, -int(ev[b, h]) - G) for h in range(Hkv)] for b in range(B)],
+                      dtype=torch.float32, device=dev)
+    dk = (dk32 * math.ldexp(1.0, -a - G)).bfloat16()
+    dv = (dv32 * sv[:, :, None, None]).bfloat16()
+    return out, dq, dk, dv, (a, ev, e, G)
 
 
 def attn_bwd_exponents(dout: torch.Tensor, ev_q: torch.Tensor, D: int):

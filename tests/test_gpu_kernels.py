@@ -237,14 +237,14 @@ def _attn_checks(q, k, v, dev, rows=None, label=""):
     ref = attn_fwd64(qd, kd, vd, True, rows=rows)
     got = o if rows is None else o[:, :, torch.as_tensor(rows, device=dev)]
     err = rel(got, ref)
-    # the reference's own result rounds O/l to fp16 before the bf16 scale-back:
-    # apply that double rounding to the exact values (a lower bound on its error)
-    evq = torch.ldexp(torch.ones_like(ev_o, dtype=torch.float64), ev_o.double()).to(dev)[..., None, None]
-    own = ((ref / evq).half().double() * evq).bfloat16()
+    # the reference's own arithmetic (fp16 P, O / l rounded to fp16, then bf16),
+    # emulated by the oracle on the same inputs and rows
+    own = O.sdpa_reference_arith(qd, kd, vd, causal=True, v_exp=13, rows=rows)
     err_own = rel(own, ref)
-    print(f"{label}: rel err {err:.3e}  reference's double rounding alone {err_own:.3e}")
+    print(f"{label}: rel err {err:.3e}  reference's own {err_own:.3e}")
     assert torch.isfinite(got).all()
     assert err <= TOL, (label, err)
+    assert err <= err_own * REF_SLACK + 1e-6, (label, err, err_own)
     return err, err_own
 
 
@@ -309,7 +309,13 @@ def test_cfg5_attention_fwd_bwd(dev):
     dq, dk, dv, ex_b = autograd.attn_backward(qv, kv, vv, o16, lse, do.to(dev), exps2, None, 128 ** -0.5, True)
     assert (int(ex_b[0]), int(ex_b[1])) == (e_o, G_o)
     ro, rdq, rdk, rdv = attn_bwd64(qv, kv, vv, do.to(dev), True)
-    for n, g_, r_ in (("o", o, ro), ("dq", qd.grad, rdq), ("dk", kd.grad, rdk), ("dv", vd.grad, rdv)):
-        e = rel(g_, r_)
-        print(f"cfg5 attention {n}: rel err {e:.3e}")
+    # the reference's own training arithmetic (fp16 out16 / dq16 / dk16 / dv16 before
+    # the bf16 scale-back), emulated by the oracle; its exponents are the closed forms
+    own_o, own_dq, own_dk, own_dv, (a_r, _, e_r, G_r) = O.sdpa_bwd_reference_arith(qv, kv, vv, do.to(dev), True)
+    assert (a_r, e_r, G_r) == (a_o, e_o, G_o)
+    for n, g_, r_, w_ in (("o", o, ro, own_o), ("dq", qd.grad, rdq, own_dq), ("dk", kd.grad, rdk, own_dk),
+                          ("dv", vd.grad, rdv, own_dv)):
+        e, eo = rel(g_, r_), rel(w_, r_)
+        print(f"cfg5 attention {n}: rel err {e:.3e}  reference's own {eo:.3e}")
         assert torch.isfinite(g_).all() and e <= TOL, (n, e)
+        assert e <= eo * REF_SLACK + 1e-6, (n, e, eo)

@@ -127,7 +127,90 @@ def test_conv_module_host_logic():
     assert not tconv.convertible(nn.Linear(4, 4))
     cls = tconv._scaled_class(nn.Conv2d)
     assert cls.__name__ == "TBF16Conv2d" and issubclass(cls, nn.Conv2d)
-    assert cls._native_conv_forward is nn.Conv2d._conv_forward and tconv._scaled_class(nn.Conv2d) is cls
+    # the scaled forward sits in front of the native one, which stays reachable through super()
+    assert cls.__mro__[1] is tconv.ScaledConvMixin and cls.__mro__[2] is nn.Conv2d
+    assert tconv._scaled_class(nn.Conv2d) is cls
     m = nn.Sequential(nn.Conv2d(4, 8, 3).bfloat16(), nn.Conv1d(4, 4, 1).bfloat16())
     tbf16.convert(m, sdpa=False, force=True)
     assert type(m[0]) is nn.Conv2d and type(m[1]) is nn.Conv1d and m[0].weight is not None
+
+
+def test_routing_predicate_shapes():
+    """The one predicate convert(), patch() and tbf16.sdpa share: shapes the fused
+    kernels do not compute (value head dim != key head dim, k/v shapes differ, GQA
+    without enable_gqa, head dim > 256) are refused with a reason; head dims that are
+    not a multiple of 8 are accepted (the caller zero-pads)."""
+    from tbf16 import routing
+    q = torch.zeros(2, 8, 32, 64)
+    kv = torch.zeros(2, 8, 40, 64)
+    assert routing.kernel_takes_qkv(q, kv, kv) is None
+    assert routing.kernel_takes_qkv(q, kv, torch.zeros(2, 8, 40, 128)) is not None  # Dv != D
+    assert routing.kernel_takes_qkv(q, kv, torch.zeros(2, 8, 41, 64)) is not None
+    assert routing.kernel_takes_qkv(q, torch.zeros(1, 8, 40, 64), torch.zeros(1, 8, 40, 64)) is not None
+    g = torch.zeros(2, 2, 40, 64)
+    assert routing.kernel_takes_qkv(q, g, g) is not None
+    assert routing.kernel_takes_qkv(q, g, g, enable_gqa=True) is None
+    g3 = torch.zeros(2, 3, 40, 64)
+    assert routing.kernel_takes_qkv(q, g3, g3, enable_gqa=True) is not None  # 8 % 3 != 0
+    big = torch.zeros(1, 1, 32, 264)
+    assert routing.kernel_takes_qkv(big, big, big) is not None
+    odd = torch.zeros(1, 1, 32, 60)
+    assert routing.kernel_takes_qkv(odd, odd, odd) is None
+    # CPU tensors always stay native
+    assert routing.attention_route(q.bfloat16(), kv.bfloat16(), kv.bfloat16()) == "native"
+    with pytest.raises(ValueError):
+        attention._check_qkv(q.bfloat16(), kv.bfloat16(), torch.zeros(2, 8, 40, 128).bfloat16(), False)
+
+
+def test_routing_bind_sdpa():
+    from tbf16 import routing
+    q, k, v = object(), object(), object()
+    c = routing.bind_sdpa((q, k), {"value": v, "is_causal": True})
+    assert c["query"] is q and c["key"] is k and c["value"] is v and c["is_causal"] is True
+    assert c["attn_mask"] is None and c["dropout_p"] == 0.0 and c["scale"] is None and c["enable_gqa"] is False
+    c = routing.bind_sdpa((), {"query": q, "key": k, "value": v, "enable_gqa": True})
+    assert c["enable_gqa"] is True
+    with pytest.raises(TypeError):
+        routing.bind_sdpa((q, k, v), {"query": q})
+    with pytest.raises(TypeError):
+        routing.bind_sdpa((q, k, v), {"bogus": 1})
+    with pytest.raises(TypeError):
+        routing.bind_sdpa((q, k), {})
+
+
+def test_native_sdpa_hook_takes_dv_different_from_d():
+    """A call torch accepts and the kernels do not (Dv != D) runs natively through the
+    installed hook instead of raising."""
+    q = torch.randn(1, 2, 32, 64).bfloat16()
+    k = torch.randn(1, 2, 32, 64).bfloat16()
+    v = torch.randn(1, 2, 32, 128).bfloat16()
+    out = convert._sdpa(q, k, v)
+    assert out.shape == (1, 2, 32, 128)
+
+
+def test_tensor_memo_semantics():
+    """TensorMemo: a hit needs the same live tensor at the same version; in-place
+    changes rebuild; freed tensors drop their entries; capacity evicts the oldest."""
+    import gc
+    from tbf16 import routing
+    memo = routing.TensorMemo(capacity=2)
+    calls = []
+
+    def build(tag):
+        calls.append(tag)
+        return tag
+
+    a = torch.zeros(4)
+    assert memo.get(a, "k", lambda: build("a1")) == "a1"
+    assert memo.get(a, "k", lambda: build("a2")) == "a1"  # hit
+    assert memo.get(a, "k2", lambda: build("a3")) == "a3"  # other key
+    a.add_(1)  # version bump
+    assert memo.get(a, "k", lambda: build("a4")) == "a4"
+    b = torch.zeros(4)
+    memo.get(b, "k", lambda: build("b1"))
+    assert len(memo) <= 2
+    n = len(memo)
+    del b
+    gc.collect()
+    assert len(memo) == n - 1  # b's entry went with it
+    assert calls == ["a1", "a3", "a4", "b1"]

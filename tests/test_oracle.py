@@ -152,7 +152,7 @@ def test_quantize_cols_matches_rows_of_transpose():
 def test_target_exps():
     assert [O.target_exp(k) for k in (1, 8, 2048, 2560, 4096, 6144, 32768, 32769, 65536, 1 << 20)] == \
         [0, 0, 0, 0, 0, 0, 0, -1, -1, -3]
-    # the bound the target is chosen for: K * 4^t <= 65504 (ops.py:41-42)
+    # the bound the target is chosen for: K * 4^t <= 65504 (ops.py:30-31)
     for K in (2048, 32768, 40000, 1 << 20):
         assert K * 4.0 ** O.target_exp(K) <= 65536
     assert O.dw_target_exp(8192) == 0 and O.dw_target_exp(40000) == -1 and O.dw_target_exp(1 << 17) == -2
@@ -209,8 +209,117 @@ def test_head_exp_and_attn_exponents_brute_force():
     a_ref = max(min(a_ref, 14 - eq), ek - 14)
     assert a == a_ref
     assert int(ev[1, 2]) == -13 and int(ev[0, 0]) == O.head_exp(v)[0, 0] - 13
-    # scaled maxima stay below 2^14 in magnitude class (attention.py:271-272)
+    # scaled maxima stay below 2^14 in magnitude class (attention.py:42-43)
     assert eq + a <= 14 and ek - a <= 14 or (ek - eq) > 28
+
+
+def _heads_with_exps(exps, S=4, D=8, seed=0):
+    """(1, H, S, D) bf16 whose head h has max |x| = 0.75 * 2^exps[h] (frexp exponent
+    exps[h]) and every other element smaller."""
+    g = torch.Generator().manual_seed(seed)
+    H = len(exps)
+    x = torch.rand(1, H, S, D, generator=g) * 0.5
+    x[0, :, 1, 2] = 0.75
+    x = x * torch.ldexp(torch.ones(H), torch.tensor(exps, dtype=torch.float32))[None, :, None, None]
+    return x.bfloat16()
+
+
+@pytest.mark.parametrize("eq,ek", [(2, 7), (7, 2), (-3, 5), (5, -3), (0, 0), (-20, 9), (9, -20), (13, 14), (1, 27)])
+def test_attn_exponent_a_balances_unclamped(eq, ek):
+    """Without clamping (eq + ek <= 28) the split puts the scaled maxima' exponents
+    eq + a and ek - a within one of each other, the key's side the larger one
+    (floor, not ceil nor truncation toward zero: (7, 2) and (2, 7) both give 1),
+    and neither above 2^14: every q.k product of the fp16 copies stays below 2^28."""
+    q = _heads_with_exps([eq - 1, eq], seed=1)
+    k = _heads_with_exps([ek, ek - 3], seed=2)
+    v = _heads_with_exps([0, 0], seed=3)
+    a, _ = O.attn_exponents(q, k, v, 13)
+    assert 0 <= (ek - a) - (eq + a) <= 1
+    assert eq + a <= 14 and ek - a <= 14
+    # the scaled copies themselves: max exponents eq + a and ek - a, all values finite
+    q16, k16, _, a2, _ = O.prepare_qkv(q, k, v, 13)
+    assert a2 == a
+    assert int(O.head_exp(q16).max()) == eq + a and int(O.head_exp(k16).max()) == ek - a
+    assert float(q16.float().abs().max()) < 2.0 ** 14 and float(k16.float().abs().max()) < 2.0 ** 14
+
+
+@pytest.mark.parametrize("eq,ek", [(10, 19), (14, 16), (15, 15), (20, 10), (30, 30), (40, -5), (-5, 40)])
+def test_attn_exponent_a_key_clamp_decides(eq, ek):
+    """eq + ek >= 29 (logits past the reference's stated 2^28 limit): the key's copy
+    is put exactly at exponent 14 (a = ek - 14), also where the query's clamp
+    14 - eq would bind first (eq + ek >= 30): the clamps' order makes the key's
+    side win. The query's copy then exceeds 2^14 (or overflows fp16)."""
+    q = _heads_with_exps([eq], seed=4)
+    k = _heads_with_exps([ek], seed=5)
+    v = _heads_with_exps([0], seed=6)
+    a, _ = O.attn_exponents(q, k, v, 0)
+    assert ek - a == 14
+    assert eq + a >= 15
+    if eq + ek >= 30:  # the case covers the query's clamp binding first
+        assert 14 - eq < math.floor((ek - eq) / 2)
+
+
+def test_attn_exponent_a_boundary_28_29():
+    """At eq + ek = 28 the balanced split still fits (both <= 14); one more and the
+    key's clamp takes over."""
+    for eq in range(-10, 30):
+        ek = 28 - eq
+        a, _ = O.attn_exponents(_heads_with_exps([eq]), _heads_with_exps([ek]), _heads_with_exps([0]), 0)
+        assert eq + a <= 14 and ek - a <= 14 and 0 <= (ek - a) - (eq + a) <= 1
+        a1, _ = O.attn_exponents(_heads_with_exps([eq]), _heads_with_exps([ek + 1]), _heads_with_exps([0]), 0)
+        assert ek + 1 - a1 == 14
+
+
+def test_reference_attention_arith_pins():
+    """The emulation of the reference's inference arithmetic: within fp16/bf16 error
+    of fp64 on peaky scaled heads; q = 0 gives the causal prefix means of V up to
+    the output roundings; its only difference from this build's arithmetic
+    (sdpa_fp16_emulated) is the fp16 rounding of O / l, so the two differ by at most
+    one fp16 rounding plus one bf16 ulp per element, and are identical where O / l is
+    exactly an fp16 value (one-hot rows copying a V row)."""
+    g = torch.Generator().manual_seed(21)
+    q = (torch.randn(1, 2, 48, 32, generator=g) * 2.0 ** 9).bfloat16()
+    k = (torch.randn(1, 2, 48, 32, generator=g) * 2.0 ** 8).bfloat16()
+    v = (torch.randn(1, 2, 48, 32, generator=g) * 2.0 ** 11).bfloat16()
+    ref = O.sdpa_ref64(q, k, v, causal=True)
+    r = O.sdpa_reference_arith(q, k, v, causal=True)
+    assert r.dtype == torch.bfloat16 and O.rel_err(r, ref) < 3e-3
+    mine, _, _ = O.sdpa_fp16_emulated(q, k, v, causal=True)
+    d = (r.double() - mine.double()).abs()
+    bound = mine.double().abs() * (2.0 ** -11 + 2.0 ** -7) + 1e-30
+    assert bool((d <= bound).all())
+    qz = torch.zeros_like(q)
+    rz = O.sdpa_reference_arith(qz, k, v, causal=True)
+    prefix = torch.cumsum(v.double(), 2) / torch.arange(1, 49, dtype=torch.float64)[:, None]
+    assert O.rel_err(rz, prefix) < 3e-3
+    # one-hot rows: P is exactly 1 on one key, O / l a bf16 V row, no rounding at all
+    S, D = 16, 16
+    qq = torch.zeros(1, 1, S, D)
+    for i in range(S):
+        qq[0, 0, i, i] = 64.0
+    vv = torch.randn(1, 1, S, D, generator=g).bfloat16()
+    ro = O.sdpa_reference_arith(qq.bfloat16(), qq.bfloat16(), vv, causal=False)
+    assert torch.equal(ro, vv)
+
+
+def test_reference_attention_bwd_arith_pins():
+    """The emulation of the reference's training attention: exponents equal the
+    closed forms (attn_exponents with v_exp = 0, attn_bwd_exponents); output and
+    gradients within fp16-level error of fp64 autograd, with GQA (the fp32 group
+    sum) and without."""
+    g = torch.Generator().manual_seed(22)
+    for H, Hkv in ((2, 2), (4, 2)):
+        q = (torch.randn(1, H, 40, 32, generator=g) * 3).bfloat16()
+        k = (torch.randn(1, Hkv, 40, 32, generator=g) * 3).bfloat16()
+        v = (torch.randn(1, Hkv, 40, 32, generator=g) * 2.0 ** 10).bfloat16()
+        do = (torch.randn(1, H, 40, 32, generator=g) * 2.0 ** -20).bfloat16()
+        o, dq, dk, dv, (a, ev, e, G) = O.sdpa_bwd_reference_arith(q, k, v, do, causal=True)
+        a0, ev0 = O.attn_exponents(q, k, v, 0)
+        e0, _, G0 = O.attn_bwd_exponents(do, O.expand_heads(ev0, H), 32)
+        assert (a, e, G) == (a0, e0, G0) and torch.equal(ev, ev0)
+        ro, rdq, rdk, rdv = O.sdpa_grads_ref64(q, k, v, do, causal=True)
+        for got, want in ((o, ro), (dq, rdq), (dk, rdk), (dv, rdv)):
+            assert torch.isfinite(got).all() and O.rel_err(got, want) < 5e-3
 
 
 def test_attention_closed_forms():

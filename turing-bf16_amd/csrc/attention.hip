@@ -1,6 +1,6 @@
 // Scaled attention forward on CDNA4 fp16 MFMA (flash-style, no S x S buffer).
 //
-// Exponents (tbf16/attention.py:267-277), computed in each block's prologue from
+// Exponents (tbf16/attention.py:38-48), computed in each block's prologue from
 // per-head partial maxima written by a memory-bound pre-pass:
 //   eq = max_{b,h} frexp(amax q[b,h]), ek likewise, a = floor((ek - eq) / 2)
 //   clamped to [ek - 14, 14 - eq], ev[b, hkv] = frexp(amax v[b, hkv]) - v_exp.
@@ -122,7 +122,7 @@ __device__ __forceinline__ uint2 gather4(uint32_t w0, uint32_t w1, uint32_t w2, 
   return make_uint2(__builtin_amdgcn_perm(w1, w0, sel), __builtin_amdgcn_perm(w3, w2, sel));
 }
 
-// Exponents (tbf16/attention.py:267-277) from the per-head partial maxima, once:
+// Exponents (tbf16/attention.py:38-48) from the per-head partial maxima, once:
 // a and ev[b * Hkv + hk] into the workspace (and into the caller's exps if given).
 // Per-head maxima of the partials, wave-parallel: wave w reduces heads w, w + 4,
 // ... (a lane per chunk), eight heads' loads in flight before any is reduced.
@@ -159,7 +159,7 @@ __device__ __forceinline__ void heads_max(const float* part, int nbh, int nch, F
 // fill each 128-byte row; the tile's DP rows are one contiguous block, which the
 // forward kernel then copies to LDS 1 KB at a time). Keys past Sk and columns
 // past D are written as zeros.
-// Each block also derives the exponents (tbf16/attention.py:267-277) from the
+// Each block also derives the exponents (tbf16/attention.py:38-48) from the
 // per-head partial maxima: a from all q and k heads, ev of its own kv head;
 // blocks (0, bhk) store them (a by block (0, 0)) to the workspace and to the
 // caller's exps, where the forward kernel and the backward read them.
@@ -477,11 +477,13 @@ attn_fwd_kernel(FwdParams p) {
           const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r + 1], c, mneg));
           pk[kh][r >> 1] = pack_f16(p0, p1);
           lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, pk[kh][r >> 1]), ones, lsum, false);
-          if constexpr (DROP) {  // l keeps the undropped weights; the PV product gets the dropped ones
+          if constexpr (DROP) {  // l keeps the undropped weights; the PV product gets the kept ones,
+            // unscaled (P reaches 2^8 under the lazy rescale: P / (1 - p) would leave fp16
+            // for p near 1), and the epilogue applies 1 / (1 - p) in fp32
             const int key = key0 + kh * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);  // even
             const uint32_t u = drop_pair(drow, key, p.drop_hi);
-            pk[kh][r >> 1] = pack_f16(drop_keep(u, key, p.drop_thr) ? p0 * p.drop_scale : 0.f,
-                                      drop_keep(u, key + 1, p.drop_thr) ? p1 * p.drop_scale : 0.f);
+            pk[kh][r >> 1] = pack_f16(drop_keep(u, key, p.drop_thr) ? p0 : 0.f,
+                                      drop_keep(u, key + 1, p.drop_thr) ? p1 : 0.f);
           }
         }
       l_run += lsum;
@@ -555,7 +557,10 @@ attn_fwd_kernel(FwdParams p) {
         if (d >= p.D) continue;
         float y[4];
   #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = l_tot > 0.f ? acc_o[db][4 * rq + e] / l_tot : 0.f;
+        for (int e = 0; e < 4; ++e) {
+          y[e] = l_tot > 0.f ? acc_o[db][4 * rq + e] / l_tot : 0.f;
+          if constexpr (DROP) y[e] *= p.drop_scale;
+        }
         *reinterpret_cast<uint2*>(p.o + orow + d) =
             make_uint2(pack_bf16(y[0] * sev, y[1] * sev), pack_bf16(y[2] * sev, y[3] * sev));
         if (p.o16) *reinterpret_cast<uint2*>(p.o16 + orow + d) = make_uint2(pack_f16(y[0], y[1]), pack_f16(y[2], y[3]));

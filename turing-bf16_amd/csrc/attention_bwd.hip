@@ -390,7 +390,7 @@ dkdv_kernel(BwdParams p) {
         pz[j] = pv[j];
         if constexpr (DROP) {
           const bool keep = drop_keep(drop_pair(dr[j], key, p.drop_hi), key, p.drop_thr);
-          pz[j] = keep ? pv[j] * p.drop_scale : 0.f;
+          pz[j] = keep ? pv[j] : 0.f;  // 1 / (1 - p) is applied to dV in fp32 at the end
           dpj = keep ? dpj * p.drop_scale : 0.f;
         }
         dsv[j] = WANT_DK ? pv[j] * (dpj - del4[j]) : 0.f;
@@ -449,8 +449,10 @@ dkdv_kernel(BwdParams p) {
     const int kind = pass >> 1, half = pass & 1;
     if ((kind == 0 && !WANT_DV) || (kind == 1 && !WANT_DK)) continue;
     floatx16* acc = kind == 0 ? dv : dk;
-    const float so = kind == 0 ? sv_out : sk_out;
-    const float chk = kind == 0 ? 1.f : p.scale;
+    // dV accumulated P o keep: the dropout scale 1 / (1 - p) comes in here, in fp32
+    const float dzs = DROP ? p.drop_scale : 1.f;
+    const float so = kind == 0 ? sv_out * dzs : sk_out;
+    const float chk = kind == 0 ? dzs : p.scale;
     if ((wave >> 1) == half) {
 #pragma unroll
       for (int db = 0; db < DB; ++db)

@@ -14,7 +14,12 @@ convolution is MIOpen's, through torch. 1x1 convolutions (stride 1, no padding,
 one group) are per-pixel linear layers and go through scaled_linear, which scales
 each pixel separately. Inference only: inputs that need gradients, or are not
 bf16, run the native convolution on the dequantized weight (conv.py:34-38).
+Converted modules get the class TBF16<their class>, the buffers weight16 and
+weight_scale and the method dequantized_weight(), as in the reference.
 """
+import functools
+from typing import NamedTuple
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -76,70 +81,81 @@ def unscale_output(y16: torch.Tensor, exps: torch.Tensor, w_sinv: torch.Tensor, 
     return out
 
 
-def _scaled_conv_forward(self, x, weight, bias):
-    """Replaces _ConvNd._conv_forward (conv.py:34-60). `weight` is the removed bf16
-    parameter (None); the fp16 copy lives in weight16."""
-    if x.dtype != torch.bfloat16 or (torch.is_grad_enabled() and x.requires_grad):
-        bias = None if bias is None else bias.to(x.dtype)
-        return self._native_conv_forward(x, self.dequantized_weight().to(x.dtype), bias)
-    nd = self.weight16.dim() - 2
-    if x.dim() == nd + 1:  # unbatched input: one sample
-        return _scaled_conv_forward(self, x.unsqueeze(0), weight, bias).squeeze(0)
-    O = self.out_channels
-    if self._tbf16_pointwise:
-        return scaled_linear(x.movedim(1, -1), self.weight16.view(O, -1), self.weight_scale, bias).movedim(-1, 1)
-    if self.padding_mode != "zeros":
-        x = F.pad(x, self._reversed_padding_repeated_twice, mode=self.padding_mode)
+class ConvPlan(NamedTuple):
+    """What convert_conv decided for one convolution."""
+    target_exp: int   # the input's per-sample target exponent (_target_exp of the weight's fan-in)
+    pointwise: bool   # 1x1, stride 1, unpadded, ungrouped: a per-pixel linear layer
+
+
+def _pointwise(conv: nn.Module) -> bool:
+    pad = conv.padding
+    unpadded = pad == "valid" or (not isinstance(pad, str) and not any(pad))
+    return unpadded and conv.groups == 1 and set(conv.kernel_size) == {1} and set(conv.stride) == {1}
+
+
+def _run_scaled(conv: nn.Module, x: torch.Tensor, bias) -> torch.Tensor:
+    """The scaled fp16 convolution of a batched bf16 input (tbf16/conv.py:39-60)."""
+    plan = conv._tbf16_plan
+    if plan.pointwise:
+        O = conv.out_channels
+        return scaled_linear(x.movedim(1, -1), conv.weight16.view(O, -1), conv.weight_scale, bias).movedim(-1, 1)
+    padding = conv.padding
+    if conv.padding_mode != "zeros":  # reflect / replicate / circular: pad first, convolve unpadded
+        x = F.pad(x, conv._reversed_padding_repeated_twice, mode=conv.padding_mode)
         padding = 0
-    else:
-        padding = self.padding
-    exps, x16 = scale_input(x, self._tbf16_target_exp)
-    y16 = _CONV[nd](x16, self.weight16, None, self.stride, padding, self.dilation, self.groups)
-    return unscale_output(y16, exps, self.weight_scale, bias)
+    exps, x16 = scale_input(x, plan.target_exp)
+    y16 = _CONV[x.dim() - 2](x16, conv.weight16, None, conv.stride, padding, conv.dilation, conv.groups)
+    return unscale_output(y16, exps, conv.weight_scale, bias)
 
 
-def _dequantized_weight(self):
-    w = self.weight16.float() * self.weight_scale.view((-1,) + (1,) * (self.weight16.dim() - 1))
-    return w.bfloat16()
+class ScaledConvMixin:
+    """First base of every converted convolution class TBF16<Conv class>
+    (tbf16/conv.py:63-78). It overrides only _conv_forward, so a subclass whose own
+    forward ends in super().forward (diffusers' causal 3-D convolutions) keeps
+    working; the class it was made from stays a base, so isinstance checks hold."""
+
+    def dequantized_weight(self) -> torch.Tensor:
+        """The bf16 weight, rebuilt exactly from weight16 and weight_scale."""
+        ws = self.weight_scale.reshape((-1,) + (1,) * (self.weight16.dim() - 1))
+        return (self.weight16.float() * ws).to(torch.bfloat16)
+
+    def _conv_forward(self, x, weight, bias):
+        # `weight` is the removed parameter (None): the weight lives in weight16
+        if x.dtype != torch.bfloat16 or (torch.is_grad_enabled() and x.requires_grad):
+            # not bf16, or a gradient is wanted: the native convolution on the rebuilt weight
+            b = None if bias is None else bias.to(x.dtype)
+            return super()._conv_forward(x, self.dequantized_weight().to(x.dtype), b)
+        if x.dim() == self.weight16.dim() - 1:  # unbatched input: one sample
+            return _run_scaled(self, x.unsqueeze(0), bias).squeeze(0)
+        return _run_scaled(self, x, bias)
 
 
-_classes = {}
-
-
-def _scaled_class(cls):
-    """A subclass of cls whose _conv_forward is the scaled one, so subclass forwards
-    that end in super().forward keep working (conv.py:71-78)."""
-    if cls not in _classes:
-        _classes[cls] = type(f"TBF16{cls.__name__}", (cls,), {
-            "_native_conv_forward": cls._conv_forward,
-            "_conv_forward": _scaled_conv_forward,
-            "dequantized_weight": _dequantized_weight,
-        })
-    return _classes[cls]
+@functools.lru_cache(maxsize=None)
+def _scaled_class(cls: type) -> type:
+    """TBF16<cls.__name__>: cls with ScaledConvMixin in front (one class per cls)."""
+    return type(f"TBF16{cls.__name__}", (ScaledConvMixin, cls), {})
 
 
 def convertible(m: nn.Module) -> bool:
-    """A bf16 nn.Conv1d/2d/3d (or subclass) on the GPU, not converted yet (conv.py:81-83)."""
-    return (isinstance(m, (nn.Conv1d, nn.Conv2d, nn.Conv3d)) and type(m) not in _classes.values()
-            and isinstance(m.weight, torch.Tensor) and m.weight.dtype == torch.bfloat16 and m.weight.is_cuda)
+    """A bf16 nn.Conv1d/2d/3d (or subclass) on the GPU that is not converted yet
+    (tbf16/conv.py:81-83)."""
+    w = getattr(m, "weight", None)
+    return (isinstance(m, (nn.Conv1d, nn.Conv2d, nn.Conv3d)) and not isinstance(m, ScaledConvMixin)
+            and isinstance(w, torch.Tensor) and w.dtype == torch.bfloat16 and w.is_cuda)
 
 
 def convert_conv(conv: nn.Module):
-    """Convert one bf16 nn.Conv{1,2,3}d (or subclass) in place (conv.py:86-103).
-    `.weight` becomes None; the buffers weight16 (fp16, the weight's shape) and
-    weight_scale (fp32 per output channel) replace it; use .dequantized_weight()."""
-    w = conv.weight.data
+    """Convert one bf16 nn.Conv{1,2,3}d (or subclass) in place and return it
+    (tbf16/conv.py:86-103). The `weight` parameter becomes None; buffers weight16
+    (fp16, the weight's shape) and weight_scale (fp32, one per output channel) hold
+    it, and .dequantized_weight() rebuilds the bf16 tensor."""
+    w = conv.weight.detach()
     O = w.shape[0]
-    K = w[0].numel()
-    t = _target_exp(K)
-    w16, ws = prepare_weight(w.reshape(O, K))
-    del conv._parameters["weight"]
-    conv.register_parameter("weight", None)
+    w16, ws = prepare_weight(w.reshape(O, -1))
+    plan = ConvPlan(_target_exp(w[0].numel()), _pointwise(conv))
+    conv.weight = None
     conv.register_buffer("weight16", w16.contiguous().view(w.shape))
     conv.register_buffer("weight_scale", ws)
-    conv._tbf16_target_exp = t
-    no_pad = conv.padding == "valid" or not isinstance(conv.padding, str) and all(p == 0 for p in conv.padding)
-    conv._tbf16_pointwise = (all(k == 1 for k in conv.kernel_size) and all(s == 1 for s in conv.stride) and no_pad
-                             and conv.groups == 1)
+    conv._tbf16_plan = plan
     conv.__class__ = _scaled_class(type(conv))
     return conv

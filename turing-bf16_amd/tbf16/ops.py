@@ -13,33 +13,35 @@ from __future__ import annotations
 
 import math
 import os
-import weakref
 
 import torch
 import torch.nn.functional as F
 
+from . import routing
 from ._ext import available, launch, ptr  # noqa: F401  (available re-exported as in the reference)
 
 # TBF16_GEMM=fused forces the max-scaled fused path for every M >= 2 (the reference's
-# switch between its fused kernel and the cuBLAS path, tbf16/ops.py:31-33). Unset:
+# switch between its fused kernel and the cuBLAS path, tbf16/ops.py:20-23). Unset:
 # M >= FUSED_MIN_M uses max row scales at t = 15, smaller M the L1 row scales.
 _GEMM = os.environ.get("TBF16_GEMM", "")
 # TBF16_GEMM_CFG=<n> pins the GEMM tile configuration (benchmarking only).
 _GEMM_CFG = int(os.environ.get("TBF16_GEMM_CFG", "-1"))
 FUSED_MIN_M = 256
-# Fused GEMM row scaling: max -> [2^14, 2^15) (tbf16/ops.py:35-37).
+# Fused GEMM row scaling: max -> [2^14, 2^15) (tbf16/ops.py:24-26).
 _FUSED_SCALE = (15, False)
-# Rows below FUSED_MIN_M: L1 norm below 2^15 (tbf16/ops.py:140-141).
+# Rows below FUSED_MIN_M: L1 norm below 2^15 (tbf16/ops.py:129-130).
 L1_TARGET = 15
-# Rows below this use the GEMV kernel (tbf16/ops.py:213-215).
+# Rows below this use the GEMV kernel (tbf16/ops.py:202-204).
 SMALL_M = 2
 
 
 def _target_exp(K: int) -> int:
-    """Rows are scaled to amax in [2^(t-1), 2^t). An fp16 GEMM output is then below
-    K * 4^t, which must stay under fp16's 65504; t = 0 covers K <= 32768
-    (tbf16/ops.py:40-43)."""
-    return min(0, (15 - math.ceil(math.log2(max(K, 1)))) // 2)
+    """Target exponent t for rows whose fp16 products are summed over K terms
+    (tbf16/ops.py:29-32). Both operands scaled below 2^t bound every partial sum by
+    K * 2^(2t); t is the largest value <= 0 with ceil(log2 K) + 2t <= 15, i.e. the
+    sum stays below 2^15 < 65504: 0 up to K = 32768, -1 up to 2^17, ..."""
+    lg = math.ceil(math.log2(max(K, 1)))
+    return min(0, (15 - lg) // 2)
 
 
 def _dev_check(*ts):
@@ -64,9 +66,11 @@ def _pad_cols(x: torch.Tensor, mult: int = 8) -> torch.Tensor:
 
 
 def quantize_rows(x: torch.Tensor, target_exp: int = 0, l1: bool = False):
-    """bf16 (R, K) -> (fp16 (R, K), fp32 (R,) inverse scales). Lossless for normal bf16 values.
-    Each row's max (or with l1=True its L1 norm) is scaled into [2^(t-1), 2^t)
-    (tbf16/ops.py:85-100)."""
+    """bf16 (R, K) -> (fp16 (R, K), fp32 (R,) inverse scales) (tbf16/ops.py:74-89).
+    Row r is multiplied by the power of two that puts its max |x| (its L1 norm with
+    l1=True) in [2^(t-1), 2^t); every bf16 value then converts exactly unless its
+    scaled magnitude falls below fp16's smallest normal 2^-14 (it becomes an fp16
+    subnormal, rounded to nearest even)."""
     assert x.dim() == 2 and x.stride(1) == 1
     _dev_check(x)
     if x.dtype != torch.bfloat16:
@@ -82,39 +86,20 @@ def quantize_rows(x: torch.Tensor, target_exp: int = 0, l1: bool = False):
     return (y if Kp == K else y[:, :K]), s_inv
 
 
-class _RowCache:
-    """Reuses quantize_rows results when the same activation feeds several linear layers
-    (Q/K/V, gate/up). Keyed by tensor identity through a weakref plus the version counter,
-    so freed or modified tensors never hit (tbf16/ops.py:118-134)."""
-
-    def __init__(self, size=8):
-        self.size, self.entries = size, []
-
-    def get(self, x, t, make):
-        for ref, ver, tt, val in self.entries:
-            if ref() is x and ver == x._version and tt == t:
-                return val
-        val = make()
-        self.entries.append((weakref.ref(x), x._version, t, val))
-        if len(self.entries) > self.size:
-            self.entries.pop(0)
-        return val
-
-
-_row_cache = _RowCache()
-
-
 def quantize_rows_shared(x: torch.Tensor, l1: bool = False):
-    """quantize_rows of x viewed as (-1, K), shared across calls on the same tensor
-    (tbf16/ops.py:144-148)."""
+    """quantize_rows(x.reshape(-1, K)) remembered per activation tensor, so the layers
+    that read one activation (Q/K/V, gate/up) quantise it once (tbf16/ops.py:107-137).
+    Max rows use t = _target_exp(K), L1 rows t = L1_TARGET; the memo is
+    routing.activations (dropped when x is freed or modified in place)."""
     K = x.shape[-1]
     t = L1_TARGET if l1 else _target_exp(K)
-    return _row_cache.get(x, (t, l1), lambda: quantize_rows(x.reshape(-1, K).contiguous(), t, l1))
+    return routing.activations.get(x, ("rows", t, bool(l1)),
+                                   lambda: quantize_rows(x.reshape(-1, K).contiguous(), t, l1))
 
 
 def prepare_weight(w: torch.Tensor):
-    """nn.Linear weight (N, K) bf16 -> (fp16 (N, K), fp32 (N,) inverse scales). Do this once
-    (tbf16/ops.py:151-153)."""
+    """nn.Linear weight (N, K) bf16 -> (fp16 (N, K), fp32 (N,) inverse scales), rows
+    max-scaled at t = _target_exp(K); done once per weight (tbf16/ops.py:140-142)."""
     return quantize_rows(w.contiguous(), _target_exp(w.shape[1]))
 
 
@@ -160,7 +145,7 @@ def _linear(x2, w16, w_sinv, bias, t, l1):
 
 def scaled_linear(x: torch.Tensor, w16: torch.Tensor, w_sinv: torch.Tensor, bias=None):
     """y = x @ W^T + b for bf16 x, with W given by prepare_weight. Returns bf16
-    (tbf16/ops.py:164-175). M < 2 -> GEMV; M >= FUSED_MIN_M -> one fused kernel with
+    (tbf16/ops.py:145-164). M < 2 -> GEMV; M >= FUSED_MIN_M -> one fused kernel with
     max row scales (t = 15); 2 <= M < FUSED_MIN_M -> the same kernel with the
     reference's L1 row scales (t = 15), fp32 accumulation and no fp16 intermediate."""
     _dev_check(x, w16, w_sinv)
@@ -179,7 +164,7 @@ def scaled_linear(x: torch.Tensor, w16: torch.Tensor, w_sinv: torch.Tensor, bias
 
 def linear_q(x16, x_sinv, w16, w_sinv, bias=None):
     """GEMM + epilogue on already-quantized rows: (x16 * x_sinv) @ (w16 * w_sinv)^T + bias,
-    bf16 (M, N) (tbf16/ops.py:178-189). fp32 accumulation, one bf16 rounding (the
+    bf16 (M, N) (tbf16/ops.py:167-178). fp32 accumulation, one bf16 rounding (the
     reference rounds to fp16 first)."""
     _dev_check(x16, w16)
     M, K = x16.shape
@@ -193,7 +178,7 @@ def linear_q(x16, x_sinv, w16, w_sinv, bias=None):
 
 
 def small_m_linear(x2: torch.Tensor, w16: torch.Tensor, w_sinv: torch.Tensor, bias=None):
-    """M = 1: GEMV in fp32 with no activation scale (tbf16/ops.py:218-229 ->
+    """M = 1: GEMV in fp32 with no activation scale (tbf16/ops.py:207-218 ->
     small_kernels.cu:107-132). M >= 2: the scaled GEMM with L1 row scales."""
     M, K = x2.shape
     if M != 1:
