@@ -160,6 +160,7 @@ def bench_small_m(iters: int):
 def bench_train(iters: int):
     import torch
     import tbf16.autograd as ag
+    from tbf16 import routing
     import workloads as W
 
     dev = torch.device("cuda", 0)
@@ -170,7 +171,7 @@ def bench_train(iters: int):
 
     def lin():
         # a training step sees a new activation every time: no quantized-x cache hits
-        ag._x_cache.entries.clear()
+        routing.activations.clear()
         xg.grad = wg.grad = None
         ag.linear(xg, wg).backward(dy)
 

@@ -145,7 +145,7 @@ CONV_CASES = [
 def test_conv_cases(dev, name, make, shape, cl):
     torch.manual_seed(0)
     tc, x, y, err = _check(dev, make(), shape, channels_last=cl)
-    if not tc._tbf16_pointwise:
+    if not tc._tbf16_plan.pointwise:
         # the scaled path is at most marginally worse than its CPU restatement
         # (the same arithmetic with the fp16 convolution's sum taken exactly)
         xin = x.cpu()
@@ -180,7 +180,7 @@ def test_conv_matches_reference_formula_on_gpu(dev):
         y = tc(x)
         amax = torch.linalg.vector_norm(x, float("inf"), dim=(1, 2, 3))
         e = torch.frexp(torch.where(amax.float() > 0, amax.float(), torch.ones_like(amax.float())))[1] \
-            - tc._tbf16_target_exp
+            - tc._tbf16_plan.target_exp
         one = torch.ones_like(amax, dtype=torch.float32)
         x16 = torch.empty_like(x, dtype=torch.float16)
         torch.mul(x, torch.ldexp(one, -e).view(2, 1, 1, 1), out=x16)
