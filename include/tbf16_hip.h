@@ -80,6 +80,18 @@ int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w
                  const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg, int32_t* exps_ws,
                  void* stream);
 
+/* tbf16_linear without a workspace argument and without allocating anything: the
+ * row exponents live in a static device array of TBF16_NOALLOC_MAX_ROWS int32 per
+ * GPU (4 MiB, held until the process ends). No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). M above the limit is rejected (TBF16_EINVAL).
+ * Calls that overlap on one GPU (concurrent streams or threads) share the array
+ * and race. Same arguments and results as tbf16_linear otherwise. */
+#define TBF16_NOALLOC_MAX_ROWS (1 << 20)
+int tbf16_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N, int64_t ldw,
+                         const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg,
+                         void* stream);
+
 /* tbf16_linear with the row exponents already computed (exps int32 (M,), e.g. by
  * tbf16_quantize_rows_t): the training forward, which quantises x once for the
  * saved fp16 copy and for the GEMM (tbf16/autograd.py:60-68). */

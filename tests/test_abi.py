@@ -75,6 +75,9 @@ def test_host_validation_rejects_before_launch():
     assert "workspace" in _err()
     assert L.tbf16_conv_epilogue(16, 2, 4, 9, 0, None, 16, None, 16, None) == -1
     assert "null" in _err()
+    # the no-allocation linear: rows beyond its static scratch are refused before any launch
+    assert L.tbf16_linear_noalloc(16, (1 << 20) + 1, 8, 8, 16, 8, 8, 16, None, 16, 8, 15, 0, -1, None) == -1
+    assert "scratch limit" in _err()
     # empty inputs launch nothing and succeed
     assert L.tbf16_conv_input(None, 0, 64, 0, None, None, None, 0, None) == 0
     assert L.tbf16_conv_epilogue(None, 0, 4, 9, 0, None, None, None, None, None) == 0

@@ -36,6 +36,7 @@
 // M <= 64 (decode) uses a separate skinny kernel that splits K across waves
 // (see skinny_kernel below).
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "abi_util.h"
@@ -807,6 +808,52 @@ extern "C" int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, co
   if (int rc = launch_row_exps(x, M, K, ldx, t, l1, exps_ws, nullptr, st)) return rc;
   return launch_gemm<true>(cfg < 0 ? pick_cfg(M, N) : cfg, x, ldx, exps_ws, nullptr, w16, ldw, ws, bias, y, ldy, M, N,
                            K, st);
+}
+
+// ---- tbf16_linear_noalloc: the row exponents in a static device array ----------
+// Each GPU the library runs on holds one copy of `scratch` (4 MiB) until the process
+// ends. Host code never passes the array's name to a kernel (on the host it is only
+// a stand-in symbol): the device address of this GPU's copy comes from
+// hipGetSymbolAddress, taken once per device with that device current, and is
+// what the kernels get. Every call on one GPU shares the array, and the row pass
+// overwrites exactly the rows a call uses before its GEMM reads them, so nothing
+// needs clearing; calls that overlap on one GPU (several streams or threads) race.
+static __device__ __align__(256) int32_t scratch[TBF16_NOALLOC_MAX_ROWS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch[kMaxDevices] = {};
+
+int scratch_ptr(int32_t** out) {
+  int dev = -1;
+  TB_CHECK(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices, "linear_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    TB_CHECK(e == hipSuccess && p != nullptr, "linear_noalloc: hipGetSymbolAddress failed (%s)", hipGetErrorString(e));
+    g_scratch[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int tbf16_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N,
+                                    int64_t ldw, const float* ws, const void* bias, void* y, int64_t ldy, int t,
+                                    int l1, int cfg, void* stream) {
+  TB_CHECK(M <= TBF16_NOALLOC_MAX_ROWS, "linear_noalloc: M = %lld rows exceeds the scratch limit of %d rows",
+           (long long)M, TBF16_NOALLOC_MAX_ROWS);
+  if (int rc = check_gemm("linear_noalloc", M, N, K, x, ldx, w16, ldw, ws, bias, y, ldy)) return rc;
+  TB_CHECK(cfg < kNumCfgs, "bad cfg");
+  if (M == 0 || N == 0) return 0;
+  int32_t* exps = nullptr;
+  if (int rc = scratch_ptr(&exps)) return rc;
+  hipStream_t st = as_stream(stream);
+  if (int rc = launch_row_exps(x, M, K, ldx, t, l1, exps, nullptr, st)) return rc;
+  return launch_gemm<true>(cfg < 0 ? pick_cfg(M, N) : cfg, x, ldx, exps, nullptr, w16, ldw, ws, bias, y, ldy, M, N, K,
+                           st);
 }
 
 extern "C" int tbf16_linear_exps(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t* exps,

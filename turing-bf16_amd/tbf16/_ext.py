@@ -39,6 +39,7 @@ _SIGS = {
     "tbf16_quantize_cols_ws_bytes": (SZ, [I64, I64]),
     "tbf16_quantize_cols_t": (I, [P, I64, I64, I64, I, P, P, I64, P, P, I64, P]),
     "tbf16_linear": (I, [P, I64, I64, I64, P, I64, I64, P, P, P, I64, I, I, I, P, P]),
+    "tbf16_linear_noalloc": (I, [P, I64, I64, I64, P, I64, I64, P, P, P, I64, I, I, I, P]),
     "tbf16_linear_exps": (I, [P, I64, I64, I64, P, P, I64, I64, P, P, P, I64, I, P]),
     "tbf16_gemm_f16": (I, [P, I64, I64, I64, P, P, I64, I64, P, P, P, I64, I, P]),
     "tbf16_gemv": (I, [P, P, I64, I64, I64, P, P, P, P]),
