@@ -6,15 +6,21 @@ Headline (BASELINE.json metric, configs[1]): the 4096^3 scaled GEMM. One step =
 one tbf16.scaled_linear call on resident bf16 inputs: the row-exponent pre-pass
 plus the fused MFMA GEMM, exactly what a caller runs (prepare_weight is done once,
 outside the timed region, as the reference's benchmark does). `value` is TFLOPS
-over K steps timed with HIP events between two synchronizations.
+over K steps timed with HIP events between two synchronizations, after W
+untimed steps; `step_median_ms` is the median of the steps timed one by one
+afterwards. The headline is measured last, after the other measurements, so that
+it sees the clocks a busy GPU holds rather than the first milliseconds after idle.
 
 Also measured (same JSON line): the 16k-token causal scaled attention forward
 (configs[3]) and its 4k variant, the small-M decode sweep in HBM GB/s (configs[2],
-weights rotated over > 256 MB so the MALL cannot hold them), and the training
-step of configs[4], and a 3x3 scaled convolution beside torch's native bf16 and fp16
-convolutions (the conv.py path; not a BASELINE config). `roofline` prices the dominant kernel (the GEMM) against the
-dense fp16 MFMA peak from its own event-timed launches; `cpu_baseline` times the
-oracle's restatement of the same workload on the host cores.
+weights rotated over > 256 MB so the MALL cannot hold them), the training step of
+configs[4], configs[0] (256 x 4096 x 4096 with outlier rows) beside its CPU
+restatement, a 3x3 scaled convolution beside torch's native bf16 and fp16
+convolutions (the conv.py path; not a BASELINE config) and torch's own fp16
+kernels on the same shapes. `roofline` prices the dominant kernel (the GEMM)
+against the dense fp16 MFMA peak from its own event-timed launches;
+`cpu_baseline` times the oracle's restatement of the headline workload on the
+host cores.
 """
 from __future__ import annotations
 
@@ -55,16 +61,41 @@ def _events_time(fn, iters: int) -> float:
     return s.elapsed_time(e) / iters
 
 
-def bench_gemm(steps: int, warmup: int):
+def _events_each(fn, iters: int) -> list:
+    """Milliseconds of each of `iters` calls of fn, every call between its own pair
+    of HIP events (back to back, one synchronization at the end)."""
+    import torch
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for i in range(iters):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(iters)]
+
+
+def gemm_inputs():
+    """configs[1]'s operands resident on the GPU, the weight prepared once."""
     import torch
     import tbf16
-    from tbf16 import _ext
     import workloads as W
 
     dev = torch.device("cuda", 0)
     x, w, _ = W.cfg2_square_gemm()
     x, w = x.to(dev), w.to(dev)
     w16, ws = tbf16.prepare_weight(w)
+    torch.cuda.synchronize()
+    return x, w16, ws
+
+
+def bench_gemm(steps: int, warmup: int, inputs):
+    import torch
+    import tbf16
+    from tbf16 import _ext
+
+    dev = torch.device("cuda", 0)
+    x, w16, ws = inputs
     M, K = x.shape
     N = w16.shape[0]
     flops = 2.0 * M * N * K
@@ -75,6 +106,8 @@ def bench_gemm(steps: int, warmup: int):
     t0 = time.perf_counter()
     ms = _events_time(lambda: tbf16.scaled_linear(x, w16, ws), steps)
     wall = time.perf_counter() - t0
+    # after it (not part of `value`): each step timed on its own, for the median
+    per_step = _events_each(lambda: tbf16.scaled_linear(x, w16, ws), max(steps, 50))
     # the dominant kernel alone: GEMM launches with precomputed row exponents
     exps = torch.empty(M, dtype=torch.int32, device=dev)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
@@ -95,7 +128,8 @@ def bench_gemm(steps: int, warmup: int):
     rows_ms = _events_time(rows_only, max(steps, 20))
     return {"ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12, "gemm_ms": gemm_ms,
             "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12, "rowscale_ms": rows_ms,
-            "rowscale_gbs": M * K * 2 / (rows_ms * 1e-3) / 1e9, "flops": flops, "wall_s": wall}
+            "rowscale_gbs": M * K * 2 / (rows_ms * 1e-3) / 1e9, "flops": flops, "wall_s": wall,
+            "step_median_ms": statistics.median(per_step), "step_samples": len(per_step)}
 
 
 def bench_attention(S: int, iters: int):
@@ -250,12 +284,54 @@ def library_ceiling():
         F.scaled_dot_product_attention(q, k, v, is_causal=True)
         ms = _events_time(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True), 10 if S > 4096 else 30)
         out[f"torch_fp16_sdpa_causal_{S}_tflops"] = round(2.0 * 16 * S * S * 128 / (ms * 1e-3) / 1e12, 1)
+    # hipBLASLt fp16 at the decode shapes of configs[2] (K = 2560, N = 10240), weights
+    # rotated over 7 copies as in the small-M bench: HBM GB/s of the same bytes
+    N, K = 10240, 2560
+    wts = [torch.randn(N, K, device=dev, dtype=torch.float16) for _ in range(7)]
+    dec = {}
+    for M in (1, 16, 64, 255):
+        xh = torch.randn(M, K, device=dev, dtype=torch.float16)
+        i = [0]
+
+        def mm():
+            xh @ wts[i[0] % 7].t()
+            i[0] += 1
+
+        for _ in range(7):
+            mm()
+        ms = _events_time(mm, 140)
+        byt = 2 * N * K + 2 * M * K + 2 * M * N
+        dec[str(M)] = {"us": round(ms * 1e3, 2), "GBs": round(byt / (ms * 1e-3) / 1e9, 1)}
+    out["torch_fp16_matmul_decode"] = dec
     return out
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _cpu_repeat(fn, min_runs: int, budget_s: float) -> tuple:
+    """Median seconds of fn over at least min_runs runs, repeating until budget_s of
+    CPU work has been spent."""
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or time.perf_counter() < t_end:
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times), len(times)
 
 
 def cpu_baseline():
     """The oracle's restatement of the fused scaled linear (quantise rows, fp32
-    matmul, scale, one bf16 rounding) on the full 4096^3 config, on the host cores."""
+    matmul, scale, one bf16 rounding) on the full 4096^3 config, on
+    the host cores: the median over ~10 s of repeated runs."""
     import torch
     import workloads as W
     from oracle import tbf16_oracle as O
@@ -264,24 +340,50 @@ def cpu_baseline():
     x, w, _ = W.cfg2_square_gemm()
     w16, ws = O.prepare_weight(w)  # once, outside the timing (as on the GPU)
     O.linear_fused(x[:64], w16, ws)
-    times = []
-    for _ in range(3):
-        t = time.perf_counter()
-        O.linear_fused(x, w16, ws)
-        times.append(time.perf_counter() - t)
-    sec = statistics.median(times)
+    sec, n = _cpu_repeat(lambda: O.linear_fused(x, w16, ws), 3, 10.0)
     fl = 2.0 * 4096 ** 3
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {"value": round(fl / sec / 1e12, 4), "unit": "TFLOPS", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"full 4096^3 scaled GEMM restatement (oracle.linear_fused: fp32 matmul), median of 3 runs, "
-                      f"{sec:.2f} s each, {cpu_model}"}
+            "sample": f"full 4096^3 scaled GEMM restatement (oracle.linear_fused: fp32 matmul), median of {n} runs, "
+                      f"{sec:.3f} s each, {_cpu_model()}"}
+
+
+def bench_cfg1():
+    """configs[0] (the reference's CPU-runnable case): 256 x 4096 x 4096 with 5 % of
+    rows scaled by 2^17, the fused path. GPU time per call (HIP events, median of 50)
+    beside the oracle's restatement of the same call on the host cores (median of 5,
+    the reference benchmark's repetition count for this config)."""
+    import torch
+    import tbf16
+    import workloads as W
+    from oracle import tbf16_oracle as O
+
+    dev = torch.device("cuda", 0)
+    x, w, _ = W.cfg1_cpu_linear()
+    xd, wd = x.to(dev), w.to(dev)
+    w16, ws = tbf16.prepare_weight(wd)
+    for _ in range(10):
+        tbf16.scaled_linear(xd, w16, ws)
+    gpu_ms = statistics.median(_events_each(lambda: tbf16.scaled_linear(xd, w16, ws), 50))
+    fl = 2.0 * 256 * 4096 * 4096
+    return {"gpu_us": round(gpu_ms * 1e3, 2), "gpu_tflops": round(fl / (gpu_ms * 1e-3) / 1e12, 2)}
+
+
+def cpu_cfg1():
+    """The CPU leg of bench_cfg1: the oracle's restatement of the same configs[0] call
+    on the host cores, median of 5 runs."""
+    import torch
+    import workloads as W
+    from oracle import tbf16_oracle as O
+
+    x, w, _ = W.cfg1_cpu_linear()
+    torch.set_num_threads(os.cpu_count() or 1)
+    w16o, wso = O.prepare_weight(w)
+    O.linear_fused(x[:16], w16o, wso)
+    sec, n = _cpu_repeat(lambda: O.linear_fused(x, w16o, wso), 5, 0.0)
+    fl = 2.0 * 256 * 4096 * 4096
+    return {"value": round(fl / sec / 1e12, 4), "unit": "TFLOPS", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"full configs[0] call (oracle.linear_fused), median of {n} runs, {sec * 1e3:.1f} ms each, "
+                      f"{_cpu_model()}"}
 
 
 def profile_run(what: str):
@@ -353,10 +455,11 @@ def main():
         profile_run(a.profile)
         return
     base = _baseline()
-    g = bench_gemm(a.steps, a.warmup)
-    print(f"[bench] gemm 4096^3: {g['tflops']:.1f} TFLOPS/step, kernel {g['gemm_tflops']:.1f} TFLOPS", file=sys.stderr,
-          flush=True)
+    gin = gemm_inputs()
     extras = {}
+    # The other measurements run first and the headline last: a GPU that has just
+    # come out of idle runs its first milliseconds of work at lower clocks, which
+    # a warm-up of a few 0.13 ms steps does not cover.
     if not a.quick:
         extras["attention_fwd"] = [bench_attention(S, it) for S, it in ((4096, 60), (16384, 20))]
         print(f"[bench] attention {extras['attention_fwd']}", file=sys.stderr, flush=True)
@@ -366,6 +469,13 @@ def main():
         print(f"[bench] train {extras['train_step']}", file=sys.stderr, flush=True)
         extras["conv_3x3"] = bench_conv(30)
         print(f"[bench] conv {extras['conv_3x3']}", file=sys.stderr, flush=True)
+        extras["configs0_linear"] = bench_cfg1()
+        print(f"[bench] configs[0] {extras['configs0_linear']}", file=sys.stderr, flush=True)
+        extras["library_ceiling"] = library_ceiling()
+        print(f"[bench] library {extras['library_ceiling']}", file=sys.stderr, flush=True)
+    g = bench_gemm(a.steps, a.warmup, gin)
+    print(f"[bench] gemm 4096^3: {g['tflops']:.1f} TFLOPS/step, kernel {g['gemm_tflops']:.1f} TFLOPS", file=sys.stderr,
+          flush=True)
     achieved = g["gemm_tflops"]
     line = {
         "metric": base["metric"],
@@ -383,8 +493,12 @@ def main():
         "config": {"workload": "4096^3 scaled GEMM (BASELINE configs[1]): row-scale pre-pass + fused fp16 MFMA GEMM",
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
         "pct_fp16_peak": round(100 * g["tflops"] / PEAK_FP16_TFLOPS, 2),
+        "step_median_ms": round(g["step_median_ms"], 4),
+        "step_median_tflops": round(g["flops"] / (g["step_median_ms"] * 1e-3) / 1e12, 1),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": traffic_from_profiles(),
+                     "traffic_source": "profiles/gemm_4096_traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                                       "per launch, calibrated on a 256 MiB device copy (not measured in this run)",
                      "kernel": "gemm_kernel<256,256,4,2,64,1,5,bf16 a> (tbf16_linear_exps): 256x256 tile, 8 waves, "
                                "k 64, 2 LDS stages, last k step deferred past the barrier, grouped MFMA schedule",
                      "kernel_us": round(g["gemm_ms"] * 1e3, 2),
@@ -392,8 +506,8 @@ def main():
         "rowscale_prepass": {"us": round(g["rowscale_ms"] * 1e3, 2), "GBs": round(g["rowscale_gbs"], 1)},
     }
     line.update(extras)
-    if not a.quick:
-        line["library_ceiling"] = library_ceiling()
+    if not a.no_cpu and not a.quick:
+        line["configs0_linear"]["cpu_baseline"] = cpu_cfg1()
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

@@ -487,7 +487,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
                                                          const uint16_t* __restrict__ B, int64_t ldb,
                                                          const float* __restrict__ b_sinv,
                                                          const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
-                                                         int64_t ldc, int M, int N, int K) {
+                                                         int64_t ldc, int M, int N, int K, int R) {
   constexpr int NT = NW * 64, NBLK = NB * MB;
   constexpr int RED = NW * NBLK * 16 * 64 * 4, TSLOT = NB * 32 * 128;  // TR: one chunk of b rows per wave
   constexpr int SMEM = TR && NW * TSLOT > RED ? NW * TSLOT : RED;
@@ -495,12 +495,16 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
   float* red = reinterpret_cast<float*>(smem);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, fh = lane >> 5;
-  const int n0 = blockIdx.x * 32 * NB;
+  // block b owns weight rows [b R, b R + R), R <= 32 NB (a multiple of 4): R below
+  // 32 NB spreads N over more blocks (one round over every CU) at the price of
+  // zero rows in the MFMA tiles, which the memory-bound decode does not notice
+  const int n0 = blockIdx.x * R;
+  const int nend = min(N, n0 + R);
   uint8_t* tslot = smem + wave * TSLOT;
 
   // rows past N (M) lie past the resources' ends and load as zeros; pieces past
   // K are zeroed by a select
-  const BufRes bres = make_res(B + (int64_t)n0 * ldb, min<int64_t>((int64_t)(N - n0) * ldb * 2, 0x7fffffff));
+  const BufRes bres = make_res(B + (int64_t)n0 * ldb, min<int64_t>((int64_t)(nend - n0) * ldb * 2, 0x7fffffff));
   const BufRes ares = make_res(A, min<int64_t>((int64_t)M * lda * 2, 0x7fffffff));
   int boff[NB], aoff[MB];
   float as[MB];
@@ -642,7 +646,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
     const int blk = g >> 8, rq = (g >> 6) & 3, ln = g & 63;
     const int nb = blk / MB, mb = blk % MB;
     const int m = 32 * mb + (ln & 31), n = n0 + 32 * nb + 8 * rq + 4 * (ln >> 5);
-    if (m >= M || n >= N) continue;
+    if (m >= M || n >= nend) continue;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < NW; ++w)
@@ -686,10 +690,25 @@ struct TileCfg {
 //     3 sets in flight 31.8 -> 30.2 us at M = 255, N = 10240, K = 2560; 4 or 6 slower)
 // and 12: 128x64, 4 waves of 64x32, k 64, 3 sets, 3 stages
 // Skinny, M <= 32: 13: 64 b rows per block, 8 waves splitting K, 3 chunks in flight
+// Skinny, M <= 64: 14: 64 b rows per block, 8 waves splitting K, 1 chunk in flight
 constexpr TileCfg kCfgs[] = {{256, 256, 32}, {128, 128, 64}, {64, 64, 64},       {128, 128, 64},    {256, 256, 32},
                              {32, 32, 64, true}, {32, 32, 64, true}, {64, 32, 64, true}, {64, 64, 64, true},
-                             {256, 256, 64}, {256, 128, 64}, {256, 64, 64}, {128, 64, 64}, {32, 64, 64, true}};
-constexpr int kNumCfgs = 14;
+                             {256, 256, 64}, {256, 128, 64}, {256, 64, 64}, {128, 64, 64}, {32, 64, 64, true},
+                             {64, 64, 64, true}};
+constexpr int kNumCfgs = 15;
+
+// Compute units of the current device (cached per device).
+int64_t num_cus() {
+  static int64_t cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
 
 // Configuration choice, fitted to measurements on MI355X (256 CUs): for M <= 64
 // with enough b rows for 160 blocks, the 64-row skinny block (8 waves splitting
@@ -704,7 +723,7 @@ int pick_cfg(int64_t M, int64_t N) {
     if (cdiv(N, 64) >= 160) return M <= 32 ? 13 : 2;
     return M <= 32 ? 6 : 7;
   }
-  constexpr int64_t kCUs = 256;
+  const int64_t kCUs = num_cus();
   constexpr int cand[] = {9, 10, 11, 12, 2};
   constexpr float eff[] = {1.0f, 0.85f, 0.7f, 0.6f, 0.45f};
   int best = 2;
@@ -741,7 +760,16 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
                 int64_t K, hipStream_t st) {
   const int bm = kCfgs[cfg].bm, bn = kCfgs[cfg].bn;
   TB_CHECK(!kCfgs[cfg].skinny || M <= bm, "gemm: configuration %d takes M <= %d", cfg, bm);
-  const int64_t blocks = kCfgs[cfg].skinny ? cdiv(N, bn) : cdiv(M, bm) * cdiv(N, bn);
+  // skinny blocks take `rows` weight rows each: as many as fit (bn) when that
+  // already fills whole rounds of blocks over the CUs, else fewer, so that the
+  // weight stream is spread over every CU in as few rounds as possible
+  int rows = bn;
+  if (kCfgs[cfg].skinny) {
+    const int64_t ncu = num_cus();
+    const int64_t rounds = cdiv(cdiv(N, bn), ncu);
+    rows = (int)std::min<int64_t>(bn, std::max<int64_t>(8, cdiv(cdiv(N, rounds * ncu), 8) * 8));
+  }
+  const int64_t blocks = kCfgs[cfg].skinny ? cdiv(N, rows) : cdiv(M, bm) * cdiv(N, bn);
   TB_CHECK(blocks < (int64_t)1 << 31, "gemm: grid too large");
   const bool even = K % kCfgs[cfg].bk == 0;  // no k-tail selects on loaded values
   const auto a = (const uint16_t*)A;
@@ -763,11 +791,12 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
     case 12: CFG(128, 64, 2, 2, 64, 3, 3); break;
 #define SKINNY(NB_, MB_, NW_, PF_, TR_)                                                                         \
   skinny_kernel<NB_, MB_, NW_, PF_, TR_, A_BF16><<<g, NW_ * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, \
-                                                                        ldc, M, N, K)
+                                                                        ldc, M, N, K, rows)
     case 5: SKINNY(1, 1, 4, 4, false); break;
     case 6: SKINNY(1, 1, 4, 4, true); break;
     case 7: SKINNY(1, 2, 4, 3, true); break;
     case 13: SKINNY(2, 1, 8, 3, true); break;
+    case 14: SKINNY(2, 2, 8, 1, true); break;
     default: SKINNY(2, 2, 4, 2, true); break;
 #undef SKINNY
 #undef CFG
