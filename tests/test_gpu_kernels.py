@@ -253,6 +253,23 @@ def test_cfg4_attention_4k(dev):
     _attn_checks(q, k, v, dev, label="cfg4 S=4096")
 
 
+@pytest.mark.parametrize("split", ["0", "1"])
+@pytest.mark.parametrize("B,H,S,D", [(1, 3, 200, 128), (2, 2, 328, 64), (1, 4, 1000, 128), (1, 2, 33, 64),
+                                     (2, 4, 2048, 128)])
+def test_attention_causal_block_forms(dev, monkeypatch, B, H, S, D, split):
+    """Both causal block forms of the forward on ragged lengths: split-key 8-wave
+    blocks (waves w and w + 4 share 32 query rows and take alternate key tiles,
+    merged through LDS) and the plain blocks, with the heavy/light pairing where
+    the grid is small. Exponents bit-exact, output against fp64 and the
+    reference's own error."""
+    monkeypatch.setenv("TBF16_ATTN_SPLIT", split)
+    g = torch.Generator().manual_seed(S + D)
+    q = (torch.randn(B, H, S, D, generator=g) * 8).bfloat16()
+    k = (torch.randn(B, H, S, D, generator=g) * 2).bfloat16()
+    v = (torch.randn(B, H, S, D, generator=g) * 300).bfloat16()
+    _attn_checks(q, k, v, dev, label=f"split={split} B={B} H={H} S={S} D={D}")
+
+
 def test_cfg4_attention_16k_sampled_rows(dev):
     q, k, v = W.cfg4_attention(16384)
     g = torch.Generator().manual_seed(5)

@@ -251,10 +251,18 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
 // Forward kernel: NW waves, 32 query rows each (BQ = 32 * NW), 64-key tiles
 // staged in two LDS stages by direct global -> LDS loads shared out over all
 // waves. NW = 8: two waves per SIMD, one block per CU; NW = 4: two blocks per CU.
-template <int DP, int NW, bool CAUSAL, bool HAS_BIAS, bool DROP>
+// SPLIT (NW = 8): waves w and w + 4 take the same 32 query rows (BQ = 128) and
+// the even and the odd key tiles respectively, from four LDS stages (a pair of
+// tiles in flight while the other pair is read); the odd group hands its O^T,
+// running max and row sums to its partner through LDS at the end. A causal grid
+// of few blocks then gets both the heavy/light pairing (every block the same
+// work) and two waves per SIMD.
+template <int DP, int NW, bool CAUSAL, bool HAS_BIAS, bool DROP, bool SPLIT = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(DP > 128 ? 1 : 2, DP > 128 ? 1 : 2))) void
 attn_fwd_kernel(FwdParams p) {
-  constexpr int NT = NW * 64, BQW = 32 * NW;
+  static_assert(!SPLIT || (NW == 8 && DP <= 128 && !HAS_BIAS && !DROP), "split-key blocks: 8 waves, no bias or dropout");
+  constexpr int RB = SPLIT ? NW / 2 : NW;  // 32-row query blocks per block
+  constexpr int NT = NW * 64, BQW = 32 * RB;
   constexpr int KS = DP / 16;            // MFMA k-steps over the head dim
   constexpr int DB = DP / 32;            // 32-wide d blocks of O^T
   constexpr int CPR = DP / 8;            // 16-byte chunks per K row
@@ -273,10 +281,13 @@ attn_fwd_kernel(FwdParams p) {
   // third stage, loads two tiles ahead, measured no faster)
   __shared__ __align__(1024) uint8_t smem0[STAGE];
   __shared__ __align__(1024) uint8_t smem1[STAGE];
-  __shared__ int red[NW];
+  __shared__ __align__(1024) uint8_t smem2[SPLIT ? STAGE : 16];
+  __shared__ __align__(1024) uint8_t smem3[SPLIT ? STAGE : 16];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int fr = lane & 31, fk = lane >> 5;
+  const int rw = SPLIT ? wave % RB : wave;  // this wave's 32-row query block
+  const int grp = SPLIT ? wave / RB : 0;    // SPLIT: key tiles of this parity
   // grid (heads, query blocks): dispatch runs over heads first, so the heaviest
   // query blocks of every head (causal) go out before any lighter one
   const int bh = blockIdx.x, b = bh / p.H, h = bh % p.H;
@@ -296,7 +307,7 @@ attn_fwd_kernel(FwdParams p) {
     const int qt = !CAUSAL ? bx : p.pair ? (pass == 0 ? ntiles - 1 - bx : bx) : (int)gridDim.y - 1 - bx;
     const int q0 = qt * BQW;
     // ---- Q fragments in registers (fp16, scaled by 2^a) ----
-    const int qrow = q0 + wave * 32 + fr;
+    const int qrow = q0 + rw * 32 + fr;
     const uint32_t drow = DROP ? drop_row((uint32_t)bh * (uint32_t)p.Sq + (uint32_t)qrow, p.drop_lo) : 0u;
     half8 qf[KS];
     {
@@ -436,7 +447,7 @@ attn_fwd_kernel(FwdParams p) {
           for (int kh = 0; kh < 2; ++kh) sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kread(kh, s), qf[s], sacc[kh], 0, 0, 0);
       }
       const int key0 = kb * BKV;
-      const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0 + wave * 32);
+      const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0 + rw * 32);
       if constexpr (HAS_BIAS) {
   #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
@@ -521,32 +532,90 @@ attn_fwd_kernel(FwdParams p) {
     // both loops start on stage 0).
     int nfull = min(nkb, p.Sk / BKV);
     if constexpr (CAUSAL) nfull = min(nfull, (q0 + 1) / BKV);
-    nfull &= ~1;
-    auto tiles = [&](int kb_begin, int kb_end, auto masked_c) {
-      // tile kb from stage cur; tile kb + 1 loads into stage nxt
-      auto one = [&](int kb, const uint8_t* cur, uint8_t* nxt) {
-        if (kb + 1 < nkb) dload(nxt, kb + 1);
-        step(kb, cur, masked_c);
-        wait_vmem();
-        __syncthreads();
+    if constexpr (SPLIT) {
+      // Super-tile j = tiles 2 j (group 0) and 2 j + 1 (group 1) in stage pair
+      // j % 2; the other pair's two loads go out when super-tile j's computation
+      // starts. Super-tiles [0, nfs) are whole for every wave (nfs even, so both
+      // loops start on stage pair 0); a group with no tile in the last super-tile
+      // still takes part in its loads and barrier.
+      const int nsup = (nkb + 1) / 2, nfs = (nfull / 2) & ~1;
+      auto supers = [&](int j_begin, int j_end, auto masked_c) {
+        auto one = [&](int j, const uint8_t* c0, const uint8_t* c1, uint8_t* n0, uint8_t* n1) {
+          if (2 * j + 2 < nkb) dload(n0, 2 * j + 2);
+          if (2 * j + 3 < nkb) dload(n1, 2 * j + 3);
+          if (2 * j + grp < nkb) step(2 * j + grp, grp ? c1 : c0, masked_c);
+          wait_vmem();
+          __syncthreads();
+        };
+        for (int j = j_begin; j < j_end; j += 2) {
+          one(j, smem0, smem1, smem2, smem3);
+          if (j + 1 < j_end) one(j + 1, smem2, smem3, smem0, smem1);
+        }
       };
-      for (int kb = kb_begin; kb < kb_end; kb += 2) {
-        one(kb, smem0, smem1);
-        if (kb + 1 < kb_end) one(kb + 1, smem1, smem0);
-      }
-    };
-    if (nkb > 0) dload(smem0, 0);
-    wait_vmem();
-    __syncthreads();
-    // (without the fragment prefetch, one loop with the masking branch keeps the
-    // register allocation within bounds)
-    if constexpr (VPRE) tiles(0, nfull, std::false_type{});
-    tiles(VPRE ? nfull : 0, nkb, std::true_type{});
+      if (nkb > 0) dload(smem0, 0);
+      if (nkb > 1) dload(smem1, 1);
+      wait_vmem();
+      __syncthreads();
+      supers(0, nfs, std::false_type{});
+      supers(nfs, nsup, std::true_type{});
+    } else {
+      nfull &= ~1;
+      auto tiles = [&](int kb_begin, int kb_end, auto masked_c) {
+        // tile kb from stage cur; tile kb + 1 loads into stage nxt
+        auto one = [&](int kb, const uint8_t* cur, uint8_t* nxt) {
+          if (kb + 1 < nkb) dload(nxt, kb + 1);
+          step(kb, cur, masked_c);
+          wait_vmem();
+          __syncthreads();
+        };
+        for (int kb = kb_begin; kb < kb_end; kb += 2) {
+          one(kb, smem0, smem1);
+          if (kb + 1 < kb_end) one(kb + 1, smem1, smem0);
+        }
+      };
+      if (nkb > 0) dload(smem0, 0);
+      wait_vmem();
+      __syncthreads();
+      // (without the fragment prefetch, one loop with the masking branch keeps the
+      // register allocation within bounds)
+      if constexpr (VPRE) tiles(0, nfull, std::false_type{});
+      tiles(VPRE ? nfull : 0, nkb, std::true_type{});
+    }
     deferred();
+
+    if constexpr (SPLIT) {
+      // Group 1's partial O^T (lane-major, DB x 16 values per lane), running max
+      // and row sums go through the idle stages; group 0 merges them into its own:
+      // m = max(m0, m1), O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise.
+      float* xo = reinterpret_cast<float*>(rw < 2 ? smem0 : smem1) + (rw & 1) * (DB * 16 * 64);
+      float* xm = reinterpret_cast<float*>(smem2) + rw * 128;
+      if (grp) {
+  #pragma unroll
+        for (int db = 0; db < DB; ++db)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) xo[(db * 16 + r) * 64 + lane] = acc_o[db][r];
+        xm[lane] = m_run;
+        xm[64 + lane] = l_run;
+      }
+      __syncthreads();
+      if (!grp) {
+        const float m1 = xm[lane], l1 = xm[64 + lane];
+        const float mm = fmaxf(m_run, m1);
+        const float a0 = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mm);
+        const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+        m_run = mm;
+        l_run = l_run * a0 + l1 * a1;
+  #pragma unroll
+        for (int db = 0; db < DB; ++db)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) acc_o[db][r] = acc_o[db][r] * a0 + xo[(db * 16 + r) * 64 + lane] * a1;
+      }
+      __syncthreads();  // the next pass reloads the stages
+    }
 
     // ---- epilogue ----
     const float l_tot = sum_xor32(l_run);
-    if (qrow < p.Sq) {
+    if ((!SPLIT || grp == 0) && qrow < p.Sq) {
     const float sev = ldexp1(ev);
     const int64_t orow = ((int64_t)bh * p.Sq + qrow) * p.D;
   #pragma unroll
@@ -599,7 +668,7 @@ WsLayout fwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64
 }
 
 template <int DP, int NW>
-int launch_fwd_nw(const FwdParams& p, bool causal, bool has_bias, dim3 grid, hipStream_t st) {
+int launch_fwd_nw(const FwdParams& p, bool causal, bool has_bias, bool split, dim3 grid, hipStream_t st) {
   // dropout kernels exist for 4-wave blocks only (the launcher picks those)
   if (p.drop_thr) {
     if constexpr (NW == 4) {
@@ -611,6 +680,8 @@ int launch_fwd_nw(const FwdParams& p, bool causal, bool has_bias, dim3 grid, hip
         else attn_fwd_kernel<DP, 4, false, false, true><<<grid, 256, 0, st>>>(p);
       }
     }
+  } else if (split) {
+    if constexpr (NW == 8 && DP <= 128) attn_fwd_kernel<DP, 8, true, false, false, true><<<grid, 512, 0, st>>>(p);
   } else if (causal) {
     if (has_bias) attn_fwd_kernel<DP, NW, true, true, false><<<grid, NW * 64, 0, st>>>(p);
     else attn_fwd_kernel<DP, NW, true, false, false><<<grid, NW * 64, 0, st>>>(p);
@@ -637,15 +708,22 @@ int launch_fwd_dp(FwdParams p, bool causal, bool has_bias, hipStream_t st, int n
   // balances many rounds); otherwise as measured above
   const bool pair = causal && tiles4 >= 2 * p.B * p.H && tiles8 < 384 && nw_override <= 0 &&
                     getenv("TBF16_ATTN_NOPAIR") == nullptr;
+  // the paired grid runs as split-key 8-wave blocks where those exist (no bias
+  // rows, no dropout, head dim <= 128); TBF16_ATTN_SPLIT=0 / 1 turns that off / on
+  // for any causal grid (benchmarking)
+  const char* sv = getenv("TBF16_ATTN_SPLIT");
+  const bool split_ok = causal && DP <= 128 && !has_bias && !p.drop_thr && nw_override <= 0;
+  const bool split = split_ok && (sv ? atoi(sv) != 0 : pair);
   int nw = nw_override > 0 ? nw_override : pair ? 4 : (tiles8 >= 128 ? 8 : 4);
   if (DP > 128 || p.drop_thr) nw = 4;
-  const int64_t ntiles = cdiv(p.Sq, nw == 8 ? 256 : 128);
-  p.pair = pair && nw == 4;
+  if (split) nw = 8;
+  const int64_t ntiles = cdiv(p.Sq, nw == 8 && !split ? 256 : 128);
+  p.pair = pair && (nw == 4 || split);
   const dim3 grid(p.B * p.H, (unsigned)(p.pair ? cdiv(ntiles, 2) : ntiles));
   if (nw == 8) {
-    if constexpr (DP <= 128) return launch_fwd_nw<DP, 8>(p, causal, has_bias, grid, st);
+    if constexpr (DP <= 128) return launch_fwd_nw<DP, 8>(p, causal, has_bias, split, grid, st);
   }
-  return launch_fwd_nw<DP, 4>(p, causal, has_bias, grid, st);
+  return launch_fwd_nw<DP, 4>(p, causal, has_bias, false, grid, st);
 }
 
 int check_bhsd(const char* fn, const char* name, const void* x, const int64_t* st, int64_t D) {

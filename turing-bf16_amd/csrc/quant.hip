@@ -176,18 +176,18 @@ __device__ __forceinline__ void head_amax_block(const uint16_t* __restrict__ x, 
   const int64_t s0 = chunk * rows_per_chunk, s1 = min(S, s0 + rows_per_chunk);
   const uint16_t* base = x + b * sb + h * sh + s0 * ss;
   const int D8 = (int)(D >> 3), n = (int)((s1 - s0) * D8);
-  // four loads in flight per thread before any of them is reduced
+  // eight loads in flight per thread before any of them is reduced
   float m0 = 0.f, m1 = 0.f;
   int i = threadIdx.x;
-  for (; i + 3 * 256 < n; i += 4 * 256) {
-    uint4 v[4];
+  for (; i + 7 * 256 < n; i += 8 * 256) {
+    uint4 v[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8; ++j) {
       const int ij = i + j * 256;
       v[j] = ldg16(base + (int64_t)(ij / D8) * ss + (ij % D8) * 8);
     }
-    m0 = fmaxf(m0, fmaxf(amax8<T>(v[0]), amax8<T>(v[1])));
-    m1 = fmaxf(m1, fmaxf(amax8<T>(v[2]), amax8<T>(v[3])));
+    m0 = fmaxf(m0, fmaxf(fmaxf(amax8<T>(v[0]), amax8<T>(v[1])), fmaxf(amax8<T>(v[2]), amax8<T>(v[3]))));
+    m1 = fmaxf(m1, fmaxf(fmaxf(amax8<T>(v[4]), amax8<T>(v[5])), fmaxf(amax8<T>(v[6]), amax8<T>(v[7]))));
   }
   for (; i < n; i += 256) m0 = fmaxf(m0, amax8<T>(ldg16(base + (int64_t)(i / D8) * ss + (i % D8) * 8)));
   float m = fmaxf(m0, m1);
@@ -325,8 +325,11 @@ int64_t col_chunks(int64_t R, int64_t K) {
   return chunks;
 }
 
+// ~512 blocks per tensor of at least 64 rows each: 32 KB a block at D = 128 (eight
+// 16-byte loads per thread), and few partials for the exponent derivation that
+// every block of the attention's conversion pass repeats
 int64_t head_chunks(int64_t BH, int64_t S) {
-  return std::max<int64_t>(1, std::min<int64_t>(cdiv(2048, std::max<int64_t>(BH, 1)), cdiv(S, 32)));
+  return std::max<int64_t>(1, std::min<int64_t>(cdiv(512, std::max<int64_t>(BH, 1)), cdiv(S, 64)));
 }
 
 }  // namespace
