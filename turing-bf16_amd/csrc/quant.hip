@@ -47,49 +47,50 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __re
   if (lane == 0) s_inv[row] = ldexp1(-p);
 }
 
-// Transposing convert: yT[c][r] = fp16((x[r][c] * rowmul[r]) * colmul[c]) over a
-// 64 x 64 tile staged through LDS; columns r in [R, ldyT) are written as zeros so
-// that the transposed operand can be consumed with a padded contraction length.
+// Transposing convert: yT[c][r] = fp16((x[r][c] * rowmul[r]) * colmul[c]). Each
+// thread converts an 8 x 8 block (eight 16-byte row loads) and transposes it in
+// registers with v_perm_b32 into eight 16-byte column stores; lane l of a wave
+// takes rows 8 (l % 8) and columns 8 (l / 8) of the wave's 64 x 64 square, so
+// every load and every store instruction moves whole 128-byte segments and no
+// LDS is involved. A block of four waves covers 64 rows x 256 columns. Rows in
+// [R, ldyT) are written as zeros, so that the transposed operand can be consumed with a padded contraction length.
 // rowmul = 2^rexp[r] or rm[r] (fp32) or 1; colmul = 2^cexp[c] or 1.
 __global__ __launch_bounds__(256) void transpose_convert_kernel(const uint16_t* __restrict__ x, int64_t R, int64_t K,
                                                                 int64_t ldx, const int32_t* __restrict__ rexp,
                                                                 const float* __restrict__ rm,
                                                                 const int32_t* __restrict__ cexp,
                                                                 uint16_t* __restrict__ yT, int64_t ldyT) {
-  __shared__ __align__(16) uint16_t tile[64][72];
-  const int tid = threadIdx.x;
-  const int64_t c0 = (int64_t)blockIdx.x * 64, r0 = (int64_t)blockIdx.y * 64;
-  // load + convert: 64 rows x 8 chunks of 8 columns, two per thread
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.y * 64 + 8 * (lane & 7);
+  const int64_t c0 = (int64_t)blockIdx.x * 256 + 64 * wave + 8 * (lane >> 3);
+  if (c0 >= K || r0 >= ldyT) return;
+  // all eight loads go out before any is used; rows >= R read row R - 1 and are
+  // written as zeros
+  uint4 v[8];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int rl = (tid >> 3) + 32 * i, cl = (tid & 7) * 8;
-    const int64_t r = r0 + rl, c = c0 + cl;
-    uint4 out = make_uint4(0, 0, 0, 0);
-    if (r < R && c < K) {
-      const uint4 v = ldg16(x + r * ldx + c);
-      const float rmul = rexp ? pow2f(rexp[r]) : (rm ? rm[r] : 1.f);
-      float cm[8];
+  for (int i = 0; i < 8; ++i) v[i] = R > 0 ? ldg16(x + min(r0 + i, R - 1) * ldx + c0) : make_uint4(0, 0, 0, 0);
+  float cm[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) cm[j] = cexp ? pow2f(cexp[c + j]) : 1.f;
-      out.x = pack_f16((bf16_lo(v.x) * rmul) * cm[0], (bf16_hi(v.x) * rmul) * cm[1]);
-      out.y = pack_f16((bf16_lo(v.y) * rmul) * cm[2], (bf16_hi(v.y) * rmul) * cm[3]);
-      out.z = pack_f16((bf16_lo(v.z) * rmul) * cm[4], (bf16_hi(v.z) * rmul) * cm[5]);
-      out.w = pack_f16((bf16_lo(v.w) * rmul) * cm[6], (bf16_hi(v.w) * rmul) * cm[7]);
-    }
-    *reinterpret_cast<uint4*>(&tile[rl][cl]) = out;
+  for (int j = 0; j < 8; ++j) cm[j] = cexp ? pow2f(cexp[c0 + j]) : 1.f;
+  uint32_t w[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = min(r0 + i, R - 1);
+    const float rmul = R <= 0 ? 0.f : rexp ? pow2f(rexp[r]) : (rm ? rm[r] : 1.f);
+    w[i][0] = pack_f16((bf16_lo(v[i].x) * rmul) * cm[0], (bf16_hi(v[i].x) * rmul) * cm[1]);
+    w[i][1] = pack_f16((bf16_lo(v[i].y) * rmul) * cm[2], (bf16_hi(v[i].y) * rmul) * cm[3]);
+    w[i][2] = pack_f16((bf16_lo(v[i].z) * rmul) * cm[4], (bf16_hi(v[i].z) * rmul) * cm[5]);
+    w[i][3] = pack_f16((bf16_lo(v[i].w) * rmul) * cm[6], (bf16_hi(v[i].w) * rmul) * cm[7]);
+    if (r0 + i >= R) w[i][0] = w[i][1] = w[i][2] = w[i][3] = 0u;
   }
-  __syncthreads();
-  // write yT rows: 64 columns x 8 chunks of 8 rows
+  // column j: dword k = (row 2k, row 2k + 1) of half j of the rows' dword j / 2
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int cl = (tid >> 3) + 32 * i, rl = (tid & 7) * 8;
-    const int64_t c = c0 + cl, r = r0 + rl;
-    if (c < K && r < ldyT) {
-      uint32_t w[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) w[j] = (uint32_t)tile[rl + 2 * j][cl] | ((uint32_t)tile[rl + 2 * j + 1][cl] << 16);
-      stg16(yT + c * ldyT + r, make_uint4(w[0], w[1], w[2], w[3]));
-    }
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    const int d = j >> 1;
+    stg16(yT + (c0 + j) * ldyT + r0,
+          make_uint4(__builtin_amdgcn_perm(w[1][d], w[0][d], sel), __builtin_amdgcn_perm(w[3][d], w[2][d], sel),
+                     __builtin_amdgcn_perm(w[5][d], w[4][d], sel), __builtin_amdgcn_perm(w[7][d], w[6][d], sel)));
   }
 }
 
@@ -400,7 +401,7 @@ extern "C" int tbf16_quantize_rows_t(const void* x, int64_t R, int64_t K, int64_
     if (int rc = launch_row_exps(x, R, K, ldx, t, 0, exps_ws, s_inv, st)) return rc;
   }
   if (K == 0 || ldyT == 0) return 0;
-  dim3 grid((unsigned)cdiv(K, 64), (unsigned)cdiv(ldyT, 64));
+  dim3 grid((unsigned)cdiv(K, 256), (unsigned)cdiv(ldyT, 64));
   transpose_convert_kernel<<<grid, 256, 0, st>>>((const uint16_t*)x, R, K, ldx, exps_ws, nullptr, nullptr,
                                                  (uint16_t*)yT, ldyT);
   TB_LAUNCH_CHECK("quantize_rows_t");
@@ -433,7 +434,7 @@ extern "C" int tbf16_quantize_cols_t(const void* x, int64_t R, int64_t K, int64_
     TB_LAUNCH_CHECK("quantize_cols/fill");
   }
   if (ldyT == 0) return 0;
-  dim3 grid((unsigned)cdiv(K, 64), (unsigned)cdiv(ldyT, 64));
+  dim3 grid((unsigned)cdiv(K, 256), (unsigned)cdiv(ldyT, 64));
   transpose_convert_kernel<<<grid, 256, 0, st>>>((const uint16_t*)x, R, K, ldx, nullptr, row_mul, cexp, (uint16_t*)yT,
                                                  ldyT);
   TB_LAUNCH_CHECK("quantize_cols/convert");
