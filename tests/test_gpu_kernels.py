@@ -253,21 +253,43 @@ def test_cfg4_attention_4k(dev):
     _attn_checks(q, k, v, dev, label="cfg4 S=4096")
 
 
+@pytest.mark.parametrize("kform", ["bf16", "fp16"])
 @pytest.mark.parametrize("split", ["0", "1"])
-@pytest.mark.parametrize("B,H,S,D", [(1, 3, 200, 128), (2, 2, 328, 64), (1, 4, 1000, 128), (1, 2, 33, 64),
-                                     (2, 4, 2048, 128)])
-def test_attention_causal_block_forms(dev, monkeypatch, B, H, S, D, split):
-    """Both causal block forms of the forward on ragged lengths: split-key 8-wave
-    blocks (waves w and w + 4 share 32 query rows and take alternate key tiles,
-    merged through LDS) and the plain blocks, with the heavy/light pairing where
-    the grid is small. Exponents bit-exact, output against fp64 and the
-    reference's own error."""
+@pytest.mark.parametrize("B,H,S,D,layout", [(1, 3, 200, 128, "bhsd"), (2, 2, 328, 64, "bshd"),
+                                            (1, 4, 1000, 128, "bshd"), (1, 2, 33, 64, "bhsd"),
+                                            (2, 4, 2048, 128, "bhsd")])
+def test_attention_causal_block_forms(dev, monkeypatch, B, H, S, D, layout, split, kform):
+    """The causal forward's block forms on ragged lengths: split-key 8-wave blocks
+    (waves w and w + 4 share 32 query rows and take alternate key tiles, merged
+    through LDS) and the plain blocks, with the heavy/light pairing where the grid
+    is small; S^T = K Q^T on the raw bf16 rows of q and k (bf16 MFMA, K tiles copied
+    from k itself, also through (B, S, H, D) strides with a key tail) and on the
+    fp16 k16 copy. Exponents bit-exact, output against fp64 and the reference's
+    own error."""
     monkeypatch.setenv("TBF16_ATTN_SPLIT", split)
+    if kform == "fp16":
+        monkeypatch.setenv("TBF16_ATTN_KF16", "1")
+    else:
+        monkeypatch.delenv("TBF16_ATTN_KF16", raising=False)
     g = torch.Generator().manual_seed(S + D)
-    q = (torch.randn(B, H, S, D, generator=g) * 8).bfloat16()
-    k = (torch.randn(B, H, S, D, generator=g) * 2).bfloat16()
-    v = (torch.randn(B, H, S, D, generator=g) * 300).bfloat16()
-    _attn_checks(q, k, v, dev, label=f"split={split} B={B} H={H} S={S} D={D}")
+    shape = (B, H, S, D) if layout == "bhsd" else (B, S, H, D)
+    q, k, v = ((torch.randn(*shape, generator=g) * m).bfloat16() for m in (8, 2, 300))
+    if layout == "bshd":  # permuted views: row stride H * D
+        q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+    _attn_checks(q, k, v, dev, label=f"split={split} k={kform} {layout} B={B} H={H} S={S} D={D}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_sdpa_without_exponents_output(dev, causal):
+    """tbf16.sdpa asks for no exponents: with bf16 K rows only V's maxima are taken.
+    Its output equals attn_forward's with the exponents requested (same kernels,
+    same V scale) and meets the fp64 bar."""
+    g = torch.Generator().manual_seed(77)
+    q, k, v = ((torch.randn(1, 4, 700, 128, generator=g) * m).bfloat16().to(dev) for m in (16, 4, 1e3))
+    o = tbf16.sdpa(q, k, v, is_causal=causal)
+    o2 = attention.attn_forward(q, k, v, None, causal, None, v_exp=13)[0]
+    assert torch.equal(o, o2)
+    assert rel(o, attn_fwd64(q, k, v, causal)) <= TOL
 
 
 def test_cfg4_attention_16k_sampled_rows(dev):

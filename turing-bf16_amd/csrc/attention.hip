@@ -69,6 +69,9 @@ struct FwdParams {
   uint16_t* o16;
   int32_t* exps;
   int pair;  // causal: block x handles query tiles ntiles-1-x and x (balanced work per block)
+  // conv_k: kv_prep writes k16 (else the forward reads k's bf16 rows directly);
+  // derive_a: the q and k partial maxima exist and kv_prep derives a from them
+  int conv_k, derive_a;
   // dropout (DROP kernels): keep iff the hashed 16-bit value >= drop_thr, kept
   // weights scaled by drop_scale = 1 / (1 - p)
   uint32_t drop_lo, drop_hi, drop_thr;
@@ -87,6 +90,20 @@ __device__ __forceinline__ int swz_k(int row, int chunk) {
 }
 
 __device__ __forceinline__ int swz_vt(int d, int chunk) { return d * 128 + ((chunk ^ ((d >> 1) & 7)) << 4); }
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// One 32x32x16 step of S^T = K Q^T: fp16 operands (k16, q 2^a), or with KBF the
+// raw bf16 rows of k and q (v_mfma_f32_32x32x16_bf16, the same rate on gfx950).
+// Scaling a bf16 value by 2^a into fp16 is exact unless it leaves fp16's normal
+// range, so both forms multiply the same values: q.k 2^(a - a).
+template <bool KBF>
+__device__ __forceinline__ floatx16 mfma_qk(half8 k, half8 q, floatx16 c) {
+  if constexpr (KBF)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, k), __builtin_bit_cast(bf16x8, q), c, 0,
+                                                    0, 0);
+  else return __builtin_amdgcn_mfma_f32_32x32x16_f16(k, q, c, 0, 0, 0);
+}
 
 // Block-wide max of an int (NT threads, one slot per wave in red).
 template <int NT>
@@ -161,6 +178,8 @@ __device__ __forceinline__ void heads_max(const float* part, int nbh, int nch, F
 // past D are written as zeros.
 // Each block also derives the exponents (tbf16/attention.py:38-48) from the
 // per-head partial maxima: a from all q and k heads, ev of its own kv head;
+// when the forward reads k's bf16 rows itself (conv_k = 0) no k16 is written,
+// and a only where the caller asks for the exponents (derive_a);
 // blocks (0, bhk) store them (a by block (0, 0)) to the workspace and to the
 // caller's exps, where the forward kernel and the backward read them.
 template <int DP>
@@ -177,11 +196,13 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
   // are in flight together with the partial-maxima loads of the exponent
   // derivation below; its first block barrier waits for both.
   uint4 kr[NKL], vr[NVB][4];
+  if (p.conv_k) {
 #pragma unroll
-  for (int i = 0; i < NKL; ++i) {
-    const int c = threadIdx.x + i * 256, row = c / CPR, ch = c % CPR;
-    const int key = key0 + row;
-    kr[i] = key < p.Sk && ch * 8 < p.D ? ldg16(kb + (int64_t)key * p.k_ss + ch * 8) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < NKL; ++i) {
+      const int c = threadIdx.x + i * 256, row = c / CPR, ch = c % CPR;
+      const int key = key0 + row;
+      kr[i] = key < p.Sk && ch * 8 < p.D ? ldg16(kb + (int64_t)key * p.k_ss + ch * 8) : make_uint4(0, 0, 0, 0);
+    }
   }
 #pragma unroll
   for (int i = 0; i < NVB; ++i) {
@@ -194,13 +215,18 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
                                                               : make_uint4(0, 0, 0, 0);
     }
   }
-  int eq = INT_MIN, ek = INT_MIN;
-  heads_max(p.part_q, p.B * p.H, p.nch_q, [&](int, float m) { eq = max(eq, frexp_exp(m)); });
-  heads_max(p.part_k, p.B * p.Hkv, p.nch_k, [&](int, float m) { ek = max(ek, frexp_exp(m)); });
-  eq = block_max_int<256>(eq, red);
-  ek = block_max_int<256>(ek, red);
-  int a = (ek - eq) >> 1;  // floor division
-  a = max(min(a, 14 - eq), ek - 14);
+  // a (tbf16/attention.py:44-45) where q's and k's maxima were taken (the caller
+  // asked for the exponents, or k16 is written); else 0, unused
+  int a = 0;
+  if (p.derive_a) {
+    int eq = INT_MIN, ek = INT_MIN;
+    heads_max(p.part_q, p.B * p.H, p.nch_q, [&](int, float m) { eq = max(eq, frexp_exp(m)); });
+    heads_max(p.part_k, p.B * p.Hkv, p.nch_k, [&](int, float m) { ek = max(ek, frexp_exp(m)); });
+    eq = block_max_int<256>(eq, red);
+    ek = block_max_int<256>(ek, red);
+    a = (ek - eq) >> 1;  // floor division
+    a = max(min(a, 14 - eq), ek - 14);
+  }
   float mv = 0.f;
   for (int c = threadIdx.x; c < p.nch_v; c += 256) mv = fmaxf(mv, p.part_v[bhk * p.nch_v + c]);
   mv = wave_max(mv);
@@ -223,10 +249,12 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
   const float sk = ldexp1(-a), sv = ldexp1(-ev);
   uint16_t* k16 = p.k16 + ((int64_t)bhk * p.Skp + key0) * DP;
   uint16_t* vt16 = p.vt16 + ((int64_t)bhk * p.Skp + key0) * DP;  // this tile's (DP, BKV) block
+  if (p.conv_k) {
 #pragma unroll
-  for (int i = 0; i < NKL; ++i) {
-    const int c = threadIdx.x + i * 256, row = c / CPR, ch = c % CPR;
-    stg16(k16 + row * DP + ch * 8, cvt_bf16x8_f16x8(kr[i], sk));
+    for (int i = 0; i < NKL; ++i) {
+      const int c = threadIdx.x + i * 256, row = c / CPR, ch = c % CPR;
+      stg16(k16 + row * DP + ch * 8, cvt_bf16x8_f16x8(kr[i], sk));
+    }
   }
 #pragma unroll
   for (int i = 0; i < NVB; ++i) {
@@ -257,10 +285,13 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
 // running max and row sums to its partner through LDS at the end. A causal grid
 // of few blocks then gets both the heavy/light pairing (every block the same
 // work) and two waves per SIMD.
-template <int DP, int NW, bool CAUSAL, bool HAS_BIAS, bool DROP, bool SPLIT = false>
+// KBF: S^T = K Q^T on the raw bf16 rows of k and q (bf16 MFMA), K tiles copied
+// straight from k (head dim = DP); only V goes through the conversion pass.
+template <int DP, int NW, bool CAUSAL, bool HAS_BIAS, bool DROP, bool SPLIT = false, bool KBF = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(DP > 128 ? 1 : 2, DP > 128 ? 1 : 2))) void
 attn_fwd_kernel(FwdParams p) {
   static_assert(!SPLIT || (NW == 8 && DP <= 128 && !HAS_BIAS && !DROP), "split-key blocks: 8 waves, no bias or dropout");
+  static_assert(!KBF || (DP <= 128 && !HAS_BIAS && !DROP), "bf16 K rows: head dim <= 128, no bias or dropout");
   constexpr int RB = SPLIT ? NW / 2 : NW;  // 32-row query blocks per block
   constexpr int NT = NW * 64, BQW = 32 * RB;
   constexpr int KS = DP / 16;            // MFMA k-steps over the head dim
@@ -316,7 +347,7 @@ attn_fwd_kernel(FwdParams p) {
       for (int s = 0; s < KS; ++s) {
         const int d = 16 * s + 8 * fk;
         uint4 v = make_uint4(0, 0, 0, 0);
-        if (qrow < p.Sq && d < p.D) v = cvt_bf16x8_f16x8(ldg16(qp + d), sq);
+        if (qrow < p.Sq && d < p.D) v = KBF ? ldg16(qp + d) : cvt_bf16x8_f16x8(ldg16(qp + d), sq);
         qf[s] = __builtin_bit_cast(half8, v);
       }
     }
@@ -328,6 +359,11 @@ attn_fwd_kernel(FwdParams p) {
     // (bi * 1024 / (2 DP) ...) for bi < KBLK, else V^T rows d.
     const int bhk = b * p.Hkv + hk;
     const BufRes kres = make_res(p.k16 + (int64_t)bhk * p.Skp * DP, min<int64_t>((int64_t)p.Skp * DP * 2, 0x7fffffff));
+    // KBF: k's own rows, stride k_ss; each tile gets a resource that starts at its
+    // first key and ends at the last key's last element, so rows past Sk read
+    // zeros (the range check covers the VGPR offset, not the SGPR one)
+    const uint16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)hk * p.k_sh;
+    const int krow = KBF ? (int)p.k_ss : DP;  // elements from one K row to the next
     const BufRes vres = make_res(p.vt16 + (int64_t)bhk * DP * p.Skp, min<int64_t>((int64_t)DP * p.Skp * 2, 0x7fffffff));
     int voff[BPW];
   #pragma unroll
@@ -336,7 +372,7 @@ attn_fwd_kernel(FwdParams p) {
       if (i < KPW) {
         const int byte = bi * 1024 + 16 * lane, row = byte / (2 * DP), phys = (byte % (2 * DP)) >> 4;
         const int lch = (swz_k<DP>(row, phys) - row * 2 * DP) >> 4;  // the XOR swizzle is its own inverse
-        voff[i] = (row * DP + lch * 8) * 2;
+        voff[i] = (row * krow + lch * 8) * 2;
       } else {
         const int byte = (bi - KBLK) * 1024 + 16 * lane, d = byte >> 7, phys = (byte & 127) >> 4;
         const int ch = (swz_vt(d, phys) - d * 128) >> 4;
@@ -345,10 +381,15 @@ attn_fwd_kernel(FwdParams p) {
     }
     auto dload = [&](uint8_t* stage, int kb) {
       const uint32_t base = lds_addr(stage);
+      const BufRes ktile =
+          KBF ? make_res(kbase + (int64_t)kb * BKV * p.k_ss,
+                         min<int64_t>(((int64_t)(p.Sk - 1 - kb * BKV) * p.k_ss + p.D) * 2, 0x7fffffff))
+              : kres;
+      const int ksoff = KBF ? 0 : kb * BKV * DP * 2;
   #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const uint32_t dst = base + (wave + NW * i) * 1024;
-        if (i < KPW) buf_load16_lds(kres, dst, voff[i], kb * BKV * DP * 2);
+        if (i < KPW) buf_load16_lds(ktile, dst, voff[i], ksoff);
         else buf_load16_lds(vres, dst, voff[i], kb * BKV * DP * 2);
       }
     };
@@ -421,7 +462,7 @@ attn_fwd_kernel(FwdParams p) {
         deferred();
   #pragma unroll
         for (int j = 0; j < NK; ++j)
-          sacc[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fq[j], qf[j >> 1], sacc[j & 1], 0, 0, 0);
+          sacc[j & 1] = mfma_qk<KBF>(fq[j], qf[j >> 1], sacc[j & 1]);
   #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
   #pragma unroll
@@ -444,7 +485,7 @@ attn_fwd_kernel(FwdParams p) {
   #pragma unroll
         for (int s = 0; s < KS; ++s)
   #pragma unroll
-          for (int kh = 0; kh < 2; ++kh) sacc[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kread(kh, s), qf[s], sacc[kh], 0, 0, 0);
+          for (int kh = 0; kh < 2; ++kh) sacc[kh] = mfma_qk<KBF>(kread(kh, s), qf[s], sacc[kh]);
       }
       const int key0 = kb * BKV;
       const bool edge = (key0 + BKV > p.Sk) || (CAUSAL && key0 + BKV - 1 > q0 + rw * 32);
@@ -681,7 +722,15 @@ int launch_fwd_nw(const FwdParams& p, bool causal, bool has_bias, bool split, di
       }
     }
   } else if (split) {
-    if constexpr (NW == 8 && DP <= 128) attn_fwd_kernel<DP, 8, true, false, false, true><<<grid, 512, 0, st>>>(p);
+    if constexpr (NW == 8 && DP <= 128) {
+      if (!p.conv_k) attn_fwd_kernel<DP, 8, true, false, false, true, true><<<grid, 512, 0, st>>>(p);
+      else attn_fwd_kernel<DP, 8, true, false, false, true><<<grid, 512, 0, st>>>(p);
+    }
+  } else if (!p.conv_k) {  // bf16 K rows (no bias rows, no dropout, head dim <= 128)
+    if constexpr (DP <= 128) {
+      if (causal) attn_fwd_kernel<DP, NW, true, false, false, false, true><<<grid, NW * 64, 0, st>>>(p);
+      else attn_fwd_kernel<DP, NW, false, false, false, false, true><<<grid, NW * 64, 0, st>>>(p);
+    }
   } else if (causal) {
     if (has_bias) attn_fwd_kernel<DP, NW, true, true, false><<<grid, NW * 64, 0, st>>>(p);
     else attn_fwd_kernel<DP, NW, true, false, false><<<grid, NW * 64, 0, st>>>(p);
@@ -763,16 +812,28 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   float* pq = reinterpret_cast<float*>(ws);
   float* pk = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_k);
   float* pv = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_v);
+  // S^T = K Q^T on k's and q's own bf16 rows where the head dim is a whole
+  // staging width and there are no bias rows or dropout (TBF16_ATTN_KF16 forces
+  // the fp16 k16 copy, for benchmarking); then q's and k's maxima are needed
+  // only for the exponents the caller asks for
+  const bool kbf = D == w.DP && w.DP <= 128 && !bias && dropout_p == 0.f && k_strides[2] < ((int64_t)1 << 23) &&
+                   getenv("TBF16_ATTN_KF16") == nullptr;
+  const bool derive_a = !kbf || exps != nullptr;
   {
-    // partial per-head maxima of q, k and v in one launch
+    // partial per-head maxima of q, k and v (or of v alone) in one launch
     AmaxSegs segs;
-    segs.n = 3;
-    segs.seg[0] = AmaxSeg{(const uint16_t*)q, B * H, H, Sq, q_strides[0], q_strides[1], q_strides[2],
-                          cdiv(Sq, w.nch_q), w.nch_q, pq};
-    segs.seg[1] = AmaxSeg{(const uint16_t*)k, B * Hkv, Hkv, Sk, k_strides[0], k_strides[1], k_strides[2],
-                          cdiv(Sk, w.nch_k), w.nch_k, pk};
-    segs.seg[2] = AmaxSeg{(const uint16_t*)v, B * Hkv, Hkv, Sk, v_strides[0], v_strides[1], v_strides[2],
-                          cdiv(Sk, w.nch_v), w.nch_v, pv};
+    segs.n = derive_a ? 3 : 1;
+    const AmaxSeg sv{(const uint16_t*)v, B * Hkv, Hkv, Sk, v_strides[0], v_strides[1], v_strides[2],
+                     cdiv(Sk, w.nch_v), w.nch_v, pv};
+    if (derive_a) {
+      segs.seg[0] = AmaxSeg{(const uint16_t*)q, B * H, H, Sq, q_strides[0], q_strides[1], q_strides[2],
+                            cdiv(Sq, w.nch_q), w.nch_q, pq};
+      segs.seg[1] = AmaxSeg{(const uint16_t*)k, B * Hkv, Hkv, Sk, k_strides[0], k_strides[1], k_strides[2],
+                            cdiv(Sk, w.nch_k), w.nch_k, pk};
+      segs.seg[2] = sv;
+    } else {
+      segs.seg[0] = sv;
+    }
     if (int rc = launch_head_amax3(segs, D, st)) return rc;
   }
   FwdParams p;
@@ -796,6 +857,8 @@ extern "C" int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64
   p.o16 = (uint16_t*)o16;
   p.exps = exps;
   p.pair = 0;
+  p.conv_k = !kbf;
+  p.derive_a = derive_a;
   set_dropout(dropout_p, seed, p.drop_lo, p.drop_hi, p.drop_thr, p.drop_scale);
   char* wsb = reinterpret_cast<char*>(ws);
   p.ex = reinterpret_cast<int32_t*>(wsb + w.off_ex);
