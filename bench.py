@@ -209,7 +209,11 @@ def bench_train(iters: int):
         xg.grad = wg.grad = None
         ag.linear(xg, wg).backward(dy)
 
-    lin()
+    # steps back to back, as in a training loop: a few untimed ones first, so the
+    # timed ones do not include the host's enqueueing of the first step on an idle
+    # GPU (~0.1 ms, a sixth of a step at 5 timed steps)
+    for _ in range(3):
+        lin()
     lin_ms = _events_time(lin, iters)
     q, k, v, do = (t.to(dev) for t in W.cfg5_train_attention())
     qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
@@ -218,7 +222,8 @@ def bench_train(iters: int):
         qg.grad = kg.grad = vg.grad = None
         ag.sdpa(qg, kg, vg, is_causal=True).backward(do)
 
-    att()
+    for _ in range(3):
+        att()
     att_ms = _events_time(att, iters)
     B, H, S, D = q.shape
     lin_fl = 6.0 * M * K * N
@@ -465,7 +470,7 @@ def main():
         print(f"[bench] attention {extras['attention_fwd']}", file=sys.stderr, flush=True)
         extras["small_m_decode"] = bench_small_m(20)
         print(f"[bench] small-M {extras['small_m_decode']}", file=sys.stderr, flush=True)
-        extras["train_step"] = bench_train(5)
+        extras["train_step"] = bench_train(20)
         print(f"[bench] train {extras['train_step']}", file=sys.stderr, flush=True)
         extras["conv_3x3"] = bench_conv(30)
         print(f"[bench] conv {extras['conv_3x3']}", file=sys.stderr, flush=True)
