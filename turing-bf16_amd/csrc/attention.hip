@@ -216,9 +216,10 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(FwdParams p) {
     }
   }
   // a (tbf16/attention.py:44-45) where q's and k's maxima were taken (the caller
-  // asked for the exponents, or k16 is written); else 0, unused
+  // asked for the exponents, or k16 is written) and this block needs it: every
+  // block that converts K, else only block (0, 0), which stores it; else 0, unused
   int a = 0;
-  if (p.derive_a) {
+  if (p.derive_a && (p.conv_k || (blockIdx.x == 0 && bhk == 0))) {
     int eq = INT_MIN, ek = INT_MIN;
     heads_max(p.part_q, p.B * p.H, p.nch_q, [&](int, float m) { eq = max(eq, frexp_exp(m)); });
     heads_max(p.part_k, p.B * p.Hkv, p.nch_k, [&](int, float m) { ek = max(ek, frexp_exp(m)); });
