@@ -382,10 +382,11 @@ attn_fwd_kernel(FwdParams p) {
     }
     auto dload = [&](uint8_t* stage, int kb) {
       const uint32_t base = lds_addr(stage);
-      const BufRes ktile =
-          KBF ? make_res(kbase + (int64_t)kb * BKV * p.k_ss,
-                         min<int64_t>(((int64_t)(p.Sk - 1 - kb * BKV) * p.k_ss + p.D) * 2, 0x7fffffff))
-              : kres;
+      // (32-bit scalar arithmetic: the tile's last row is at most BKV - 1 rows on,
+      // and the launcher keeps BKV rows of k within 2^31 bytes; 64-bit forms
+      // compile to vector code and a waterfall loop around every load)
+      const int last = min(p.Sk - 1 - kb * BKV, BKV - 1);
+      const BufRes ktile = KBF ? make_res(kbase + (int64_t)kb * BKV * p.k_ss, (last * krow + p.D) * 2) : kres;
       const int ksoff = KBF ? 0 : kb * BKV * DP * 2;
   #pragma unroll
       for (int i = 0; i < BPW; ++i) {
