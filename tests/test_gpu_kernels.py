@@ -279,6 +279,24 @@ def test_attention_causal_block_forms(dev, monkeypatch, B, H, S, D, layout, spli
     _attn_checks(q, k, v, dev, label=f"split={split} k={kform} {layout} B={B} H={H} S={S} D={D}")
 
 
+@pytest.mark.parametrize("kform", ["bf16", "fp16"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_sdpa_gqa_key_forms(dev, monkeypatch, causal, kform):
+    """Grouped-query attention (8 query heads on 2 key/value heads, a key tail)
+    through tbf16.sdpa with K read as bf16 rows or as the fp16 k16 copy: within the
+    fp64 bar, and the two forms within each other's rounding."""
+    if kform == "fp16":
+        monkeypatch.setenv("TBF16_ATTN_KF16", "1")
+    else:
+        monkeypatch.delenv("TBF16_ATTN_KF16", raising=False)
+    g = torch.Generator().manual_seed(91)
+    q = (torch.randn(2, 8, 333, 128, generator=g) * 6).bfloat16().to(dev)
+    k = (torch.randn(2, 2, 333, 128, generator=g) * 3).bfloat16().to(dev)
+    v = (torch.randn(2, 2, 333, 128, generator=g) * 50).bfloat16().to(dev)
+    o = tbf16.sdpa(q, k, v, is_causal=causal, enable_gqa=True)
+    assert rel(o, attn_fwd64(q, k, v, causal)) <= TOL
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_sdpa_without_exponents_output(dev, causal):
     """tbf16.sdpa asks for no exponents: with bf16 K rows only V's maxima are taken.
