@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TBF16_ABI_VERSION 1
+#define TBF16_ABI_VERSION 2
 
 #define TBF16_OK 0
 #define TBF16_EINVAL (-1) /* bad shape, stride, alignment or dtype */
@@ -71,23 +71,30 @@ int tbf16_quantize_cols_t(const void* x, int64_t R, int64_t K, int64_t ldx, int 
 
 /* Fused scaled linear: y = bf16((sum_k fp16(x[m,k] * 2^p[m]) * w16[n,k]) * 2^-p[m]
  * * ws[n] + bias[n]), fp16 MFMA with fp32 accumulation, p from tbf16_row_exps(x, t,
- * l1) computed inside this call into exps_ws (int32 (M,)). One bf16 rounding.
+ * l1) computed inside this call. One bf16 rounding.
  * x bf16 (M, K); w16 fp16 (N, K); ws fp32 (N,); bias bf16 (N,) or NULL; y bf16
- * (M, N). cfg < 0 picks the tile shape. Replaces linear (tbf16/csrc/gemm_sm75.cu:
- * 257-284) and, at 2 <= M < 256, quantize_rows + cuBLAS + epilogue
- * (tbf16/ops.py:163-178) without its fp16 intermediate. */
+ * (M, N). cfg < 0 picks the tile shape. workspace: tbf16_linear_ws_bytes(M, K, N,
+ * cfg) bytes, 16-byte aligned; its first M int32 receive the row exponents p (the
+ * decode configurations also keep x's scaled fp16 copy there, as the reference's
+ * small-M path does). Replaces linear (tbf16/csrc/gemm_sm75.cu:257-284) and, at
+ * 2 <= M < 256, quantize_rows + cuBLAS + epilogue (tbf16/ops.py:163-178) without
+ * its fp16 intermediate. */
+size_t tbf16_linear_ws_bytes(int64_t M, int64_t K, int64_t N, int cfg);
 int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N, int64_t ldw,
-                 const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg, int32_t* exps_ws,
+                 const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg, void* workspace,
                  void* stream);
 
 /* tbf16_linear without a workspace argument and without allocating anything: the
- * row exponents live in a static device array of TBF16_NOALLOC_MAX_ROWS int32 per
- * GPU (4 MiB, held until the process ends). No counterpart in the reference: it is
+ * workspace lives in a static device array of TBF16_NOALLOC_SCRATCH_BYTES per GPU
+ * (12 MiB, held until the process ends). No counterpart in the reference: it is
  * for callers that cannot allocate (code under HIP graph capture, serving loops,
- * harnesses that forbid hipMalloc). M above the limit is rejected (TBF16_EINVAL).
- * Calls that overlap on one GPU (concurrent streams or threads) share the array
- * and race. Same arguments and results as tbf16_linear otherwise. */
+ * harnesses that forbid hipMalloc). M above TBF16_NOALLOC_MAX_ROWS, or a call whose
+ * tbf16_linear_ws_bytes exceeds the array (decode-sized M with K beyond ~24k), is
+ * rejected (TBF16_EINVAL). Calls that overlap on one GPU (concurrent streams or
+ * threads) share the array and race. Same arguments and results as tbf16_linear
+ * otherwise. */
 #define TBF16_NOALLOC_MAX_ROWS (1 << 20)
+#define TBF16_NOALLOC_SCRATCH_BYTES (12 << 20)
 int tbf16_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N, int64_t ldw,
                          const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg,
                          void* stream);

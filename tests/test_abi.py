@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _ext.lib().tbf16_abi_version() == _ext.ABI_VERSION == 1
+    assert _ext.lib().tbf16_abi_version() == _ext.ABI_VERSION == 2
 
 
 def _err():

@@ -37,6 +37,13 @@ def row_exps_gpu(x: torch.Tensor, t: int, l1: bool) -> np.ndarray:
     return e.cpu().numpy()
 
 
+def linear_ws(M, K, N, cfg, dev):
+    """tbf16_linear's workspace (bytes) and the int32 view of its row exponents."""
+    b = int(_ext.lib().tbf16_linear_ws_bytes(M, K, N, cfg))
+    w = torch.full((b,), 0xAB, dtype=torch.uint8, device=dev)
+    return w, w[: 4 * M].view(torch.int32)
+
+
 def test_native_library_is_the_one_loaded(dev):
     assert _ext.available()
     p = _ext.lib_path()
@@ -98,9 +105,11 @@ def test_quantize_rows_t_and_cols_t_bit_exact(dev):
 
 # ---- MFMA layout and epilogue: exact small-integer GEMMs -------------------------
 
-# tiled configurations take any M; skinny ones (5-8, 13, 14) M <= 32 or 64
+# tiled configurations take any M; skinny ones (5-8, 13, 14) M <= 32 or 64; the
+# decode ones (15-18, fp16 a) any M, in row tiles of 32 / 64 / 128 / 256
 GEMM_CFG_M = {0: 300, 1: 300, 2: 300, 3: 300, 4: 300, 5: 29, 6: 29, 7: 61, 8: 61, 9: 300, 10: 300, 11: 300, 12: 300,
-              13: 29, 14: 61}
+              13: 29, 14: 61, 15: 300, 16: 300, 17: 300, 18: 300}
+STREAM_CFGS = (15, 16, 17, 18)
 
 
 @pytest.mark.parametrize("K", [200, 1000, 3040])
@@ -129,13 +138,15 @@ def test_gemm_small_integers_bit_exact(dev, cfg, K):
     _ext.call("tbf16_gemm_f16", a16.data_ptr(), M, K, K, sad.data_ptr(), b16.data_ptr(), N, K, sbd.data_ptr(),
               bd.data_ptr(), y.data_ptr(), N, cfg, _ext.stream())
     assert torch.equal(y.cpu(), want)
-    # bf16 activations through the fused path: row max 1 -> scale 2^14, exact
+    # bf16 activations through the fused path (the decode configurations: through the
+    # workspace's fp16 copy): row max 1 -> scale 2^14, exact
     xb = a.bfloat16().to(dev)
-    e = torch.empty(M, dtype=torch.int32, device=dev)
+    work, e = linear_ws(M, K, N, cfg, dev)
     ones = torch.ones(N, device=dev)
     _ext.call("tbf16_linear", xb.data_ptr(), M, K, K, b16.data_ptr(), N, K, ones.data_ptr(), None, y.data_ptr(), N, 15,
-              0, cfg, e.data_ptr(), _ext.stream())
+              0, cfg, work.data_ptr(), _ext.stream())
     assert torch.equal(y.cpu(), (a @ b.t()).double().bfloat16())
+    assert np.array_equal(e.cpu().numpy(), O.row_exps(a.bfloat16(), 15))
 
 
 def test_gemv_small_integers_bit_exact(dev):
@@ -194,16 +205,18 @@ def test_cfg3_small_m(dev, M):
     _linear_checks(xs[M], w, dev, f"cfg3 M={M}")
 
 
-@pytest.mark.parametrize("cfg", [-1, 5, 6, 7, 13])
+@pytest.mark.parametrize("cfg,M", [(-1, 29), (-1, 61), (-1, 128), (-1, 255), (5, 29), (6, 29), (7, 61), (13, 29),
+                                   (15, 29), (16, 61), (17, 100), (18, 255)])
 @pytest.mark.parametrize("l1", [0, 1])
-def test_skinny_row_exponents_and_output(dev, cfg, l1):
-    """Decode-sized tbf16_linear on the skinny configurations: the row exponents it
-    leaves in the caller's workspace equal the oracle's bit for bit (max and L1
-    rows, K not a multiple of 64, rows spanning 2^-30 .. 2^30, a zero row), and the
-    output equals the same kernel run on those exponents (tbf16_linear_exps)."""
-    g = torch.Generator().manual_seed(7 + l1)
-    M = 29 if cfg in (-1, 5, 6, 13) else 61
-    N, K = 10240 if cfg == -1 else 264, 2504
+def test_decode_row_exponents_and_output(dev, cfg, M, l1):
+    """Decode-sized tbf16_linear on the skinny and decode configurations and on the
+    dispatcher's own choice: the row exponents it leaves in the caller's workspace
+    equal the oracle's bit for bit (max and L1 rows, K not a multiple of 64, rows
+    spanning 2^-30 .. 2^30, a zero row), and the output equals the same kernel run
+    on those exponents (tbf16_linear_exps), or for the configurations that take fp16
+    a, on quantize_rows' fp16 copy (tbf16_gemm_f16)."""
+    g = torch.Generator().manual_seed(7 + l1 + M)
+    N, K = 10240 if cfg in (-1, 18) else 264, 2504
     x = (torch.randn(M, K, generator=g) * torch.ldexp(torch.ones(M, 1), torch.randint(-30, 31, (M, 1), generator=g))
          ).bfloat16()
     x[3] = 0.0
@@ -211,15 +224,22 @@ def test_skinny_row_exponents_and_output(dev, cfg, l1):
     xd, wd = x.to(dev), w.to(dev)
     w16, ws = ops.prepare_weight(wd)
     y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    e = torch.full((M,), -999, dtype=torch.int32, device=dev)
+    work, e = linear_ws(M, K, N, cfg, dev)
+    e.fill_(-999)
     _ext.call("tbf16_linear", xd.data_ptr(), M, K, K, w16.data_ptr(), N, K, ws.data_ptr(), None, y.data_ptr(), N, 15,
-              l1, cfg, e.data_ptr(), _ext.stream())
+              l1, cfg, work.data_ptr(), _ext.stream())
     torch.cuda.synchronize()
     assert np.array_equal(e.cpu().numpy(), O.row_exps(x, 15, bool(l1)))
-    c = cfg if cfg >= 0 else 13
     y2 = torch.empty_like(y)
-    _ext.call("tbf16_linear_exps", xd.data_ptr(), M, K, K, e.data_ptr(), w16.data_ptr(), N, K, ws.data_ptr(), None,
-              y2.data_ptr(), N, c, _ext.stream())
+    L = _ext.lib()
+    # a configuration that takes fp16 a needs a larger workspace than skinny cfg 13
+    if cfg in STREAM_CFGS or L.tbf16_linear_ws_bytes(M, K, N, cfg) != L.tbf16_linear_ws_bytes(M, K, N, 13):
+        x16, sx = ops.quantize_rows(xd, 15, bool(l1))
+        _ext.call("tbf16_gemm_f16", x16.data_ptr(), M, K, K, sx.data_ptr(), w16.data_ptr(), N, K, ws.data_ptr(),
+                  None, y2.data_ptr(), N, cfg, _ext.stream())
+    else:
+        _ext.call("tbf16_linear_exps", xd.data_ptr(), M, K, K, e.data_ptr(), w16.data_ptr(), N, K, ws.data_ptr(),
+                  None, y2.data_ptr(), N, cfg, _ext.stream())
     assert torch.equal(y, y2)
     ref = (x.double() @ (w16.cpu().double() * ws.cpu().double()[:, None]).t())
     assert rel(y.cpu(), ref) < TOL

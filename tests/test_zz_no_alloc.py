@@ -1,7 +1,7 @@
-"""tbf16_linear_noalloc (row exponents in the library's static device scratch array)
-against tbf16_linear (row exponents in a caller workspace): the same output bit for
-bit on two calls in a row, the second one smaller, through the C ABI; and rows
-beyond the scratch limit are rejected before any launch."""
+"""tbf16_linear_noalloc (its workspace in the library's static device scratch array)
+against tbf16_linear (workspace from the caller): the same output bit for bit on two
+calls in a row, the second one smaller, through the C ABI; and calls beyond the
+scratch limit are rejected before any launch."""
 import ctypes
 
 import pytest
@@ -26,9 +26,9 @@ def _with_workspace(x, w16, ws, b, t, l1):
     M, K = x.shape
     N = w16.shape[0]
     y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
-    e = torch.empty(M, dtype=torch.int32, device=x.device)
+    work = torch.empty(int(_ext.lib().tbf16_linear_ws_bytes(M, K, N, -1)), dtype=torch.uint8, device=x.device)
     _ext.call("tbf16_linear", x.data_ptr(), M, K, K, w16.data_ptr(), N, K, ws.data_ptr(), b.data_ptr(), y.data_ptr(),
-              N, t, l1, -1, e.data_ptr(), _ext.stream())
+              N, t, l1, -1, work.data_ptr(), _ext.stream())
     return y
 
 
@@ -56,4 +56,9 @@ def test_noalloc_rejects_rows_beyond_limit(dev):
     L = _ext.lib()
     limit = 1 << 20
     rc = L.tbf16_linear_noalloc(16, limit + 1, 8, 8, 16, 8, 8, 16, None, 16, 8, 15, 0, -1, None)
+    assert rc == -1 and "scratch limit" in L.tbf16_last_error().decode()
+    # a decode-sized call whose fp16 copy of x would not fit the array
+    K = 32768
+    assert L.tbf16_linear_ws_bytes(255, K, 10240, 18) > (12 << 20)
+    rc = L.tbf16_linear_noalloc(16, 255, K, K, 16, 10240, K, 16, None, 16, 10240, 15, 1, 18, None)
     assert rc == -1 and "scratch limit" in L.tbf16_last_error().decode()

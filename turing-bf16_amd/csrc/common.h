@@ -182,6 +182,22 @@ __device__ __forceinline__ void wait_vmem() {
   static_assert(N >= 0 && N <= 15, "vmcnt immediate");
   __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
+// s_waitcnt vmcnt(N) for N up to 63 (gfx9 encoding: vmcnt bits [3:0] and [15:14]),
+// expcnt and lgkmcnt left at their maxima
+template <int N>
+__device__ __forceinline__ void wait_vmem_n() {
+  static_assert(N >= 0 && N <= 63, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+// Workgroup barrier without the memory fence of __syncthreads (which waits for
+// every outstanding load, direct-to-LDS loads in flight included). The caller
+// waits for whatever the other waves must see (s_waitcnt) before it; the empty
+// asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void barrier_no_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 // LDS byte address of a __shared__ object
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const lds_void*)p;

@@ -668,9 +668,182 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(const uint16_t* __restr
   }
 }
 
+// Decode GEMM on fp16 operands (a16 already scaled and converted by the row pass,
+// so neither operand needs VALU work): M up to a few hundred rows against a long
+// weight stream. One block per R rows of b (R <= 64, chosen by the launcher so the
+// blocks cover every CU once) and MT rows of a (grid.y = ceil(M / MT)). Both
+// operands go global -> LDS by direct 16-byte buffer loads (buffer_load_dwordx4
+// ... lds) into a ring of S k-tile stages, S - 1 tiles in flight per block and no
+// VGPRs holding data in flight, so a CU keeps ~120 KB of loads outstanding; one
+// barrier per k tile. LDS tile rows are 64 fp16 (128 bytes) with the 16-byte chunk
+// index XOR-swizzled by (row / 2) % 8 (the direct loads apply the swizzle on the
+// source side: lane j of a load lands at byte 16 j of its 1 KB block). MT <= 64:
+// the four waves split each tile's four 16-wide k steps and their partial tiles
+// are summed through LDS at the end; MT >= 128: each wave owns MT / 4 rows of a.
+// Rows of b past R, rows of a past M and k past K load as zeros (past the end of
+// the tile's buffer resource). The result is staged in LDS as bf16 rows and
+// written in whole 16-byte lanes.
+template <int MT, int S>
+__global__ __launch_bounds__(256) void stream_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                     const float* __restrict__ a_sinv, const uint16_t* __restrict__ B,
+                                                     int64_t ldb, const float* __restrict__ b_sinv,
+                                                     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C,
+                                                     int64_t ldc, int M, int N, int K, int R) {
+  constexpr int NP = 64;                      // LDS rows of b
+  constexpr int STG = (MT + NP) * 128;        // one k tile of both operands
+  constexpr int WK = MT <= 64 ? 4 : 1;        // waves splitting a tile's k steps
+  constexpr int TM = MT * WK / 4;             // rows of a per wave
+  constexpr int FM = TM / 32, FN = NP / 32;   // 32x32 MFMA blocks per wave
+  constexpr int LW = (MT + NP) / 32;          // direct loads per wave per tile
+  constexpr int LA = MT / 32;                 // the first LA of them are rows of a
+  constexpr int OP = NP * 2 + 16;             // pitch of the bf16 output rows in LDS
+  static_assert(S >= 3 && S <= 12 && MT % 32 == 0 && (WK == 1 || S >= 5), "stream shape");
+  static_assert(FN * FM * 16 * 64 * 4 <= STG && MT * OP <= STG, "epilogue staging fits a stage");
+  // one __shared__ object per stage: the compiler tracks direct-to-LDS loads per
+  // object, so reading one stage never waits for the loads into the others
+  __shared__ __align__(1024) uint8_t st0[STG], st1[STG], st2[STG];
+  __shared__ __align__(1024) uint8_t st3[S > 3 ? STG : 16], st4[S > 4 ? STG : 16], st5[S > 5 ? STG : 16];
+  __shared__ __align__(1024) uint8_t st6[S > 6 ? STG : 16], st7[S > 7 ? STG : 16], st8[S > 8 ? STG : 16];
+  __shared__ __align__(1024) uint8_t st9[S > 9 ? STG : 16], st10[S > 10 ? STG : 16], st11[S > 11 ? STG : 16];
+  uint8_t* const stages[12] = {st0, st1, st2, st3, st4, st5, st6, st7, st8, st9, st10, st11};
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n0 = blockIdx.x * R, m0 = blockIdx.y * MT;
+  const int nrows = min(R, N - n0), mrows = min(MT, M - m0);
+  const BufRes ares = make_res(A + (int64_t)m0 * lda, (int64_t)mrows * lda * 2);
+  const BufRes bres = make_res(B + (int64_t)n0 * ldb, (int64_t)nrows * ldb * 2);
+  // load j of wave w fills 1 KB block w + 4 j of the stage: rows 8 (w + 4 j) + lane / 8
+  // of the stacked [a rows | b rows] tile, physical chunk lane % 8, which holds
+  // logical chunk `chunk` (the same for every load of this wave)
+  const int chunk = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
+  int voff[LW];
+#pragma unroll
+  for (int j = 0; j < LW; ++j) {
+    const int row = 8 * (wave + 4 * j) + (lane >> 3);
+    voff[j] = j < LA ? (row * (int)lda + chunk * 8) * 2 : ((row - MT) * (int)ldb + chunk * 8) * 2;
+  }
+  auto issue = [&](uint8_t* stage, int kt) {
+    const uint32_t base = lds_addr(stage);
+    const bool kok = kt * 64 + chunk * 8 < K;  // a k tail reads zeros (offset past any resource)
+#pragma unroll
+    for (int j = 0; j < LW; ++j)
+      buf_load16_lds(j < LA ? ares : bres, base + (wave + 4 * j) * 1024, kok ? voff[j] : (int)0x80000000, kt * 128);
+  };
+
+  floatx16 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  const int fr = lane & 31, fk = lane >> 5;
+  const int wm = WK == 1 ? wave : 0;
+  auto compute = [&](const uint8_t* stage) {
+#pragma unroll
+    for (int s = 0; s < 4 / WK; ++s) {
+      const int c = 2 * (WK == 1 ? s : wave) + fk;
+      half8 bf[FN], af[FM];
+#pragma unroll
+      for (int i = 0; i < FN; ++i) bf[i] = *reinterpret_cast<const half8*>(stage + swz<64>(MT + i * 32 + fr, c));
+#pragma unroll
+      for (int j = 0; j < FM; ++j) af[j] = *reinterpret_cast<const half8*>(stage + swz<64>(wm * TM + j * 32 + fr, c));
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[i], af[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int KT = (K + 63) / 64;
+#pragma unroll
+  for (int u = 0; u < S - 1; ++u)
+    if (u < KT) issue(stages[u], u);
+  for (int kt0 = 0; kt0 < KT; kt0 += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int kt = kt0 + u;
+      if (kt < KT) {
+        // this wave's loads of tile kt have landed once no more than the later
+        // tiles' loads (up to S - 2 tiles, fewer at the end) are outstanding
+        if (kt + S - 2 < KT) wait_vmem_n<LW * (S - 2)>();
+        else wait_vmem_n<0>();
+        // tile kt complete in LDS; every wave is past tile kt - 1 (a bare barrier:
+        // __syncthreads' workgroup fence would wait for every load in flight)
+        barrier_no_fence();
+        if (kt + S - 1 < KT) issue(stages[(u + S - 1) % S], kt + S - 1);
+        compute(stages[u]);
+      }
+    }
+  }
+  __syncthreads();  // the stages are reused below
+
+  // ---- epilogue: (acc * sa[m]) * sb[n] + bias[n] -> bf16 rows in LDS -> C ----
+  uint8_t* otile = WK > 1 ? st4 : st0;
+  auto final_store = [&](int ml, int nl, const float (&v)[4]) {
+    const int m = m0 + ml, n = n0 + nl;
+    const float sa = m < M ? a_sinv[m] : 0.f;
+    float4 sb = make_float4(0.f, 0.f, 0.f, 0.f);
+    float bb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (nl < nrows) {
+      sb = *reinterpret_cast<const float4*>(b_sinv + n);
+      if (bias) {
+        const uint32_t b01 = *reinterpret_cast<const uint32_t*>(bias + n);
+        const uint32_t b23 = *reinterpret_cast<const uint32_t*>(bias + n + 2);
+        bb[0] = bf16_lo(b01); bb[1] = bf16_hi(b01); bb[2] = bf16_lo(b23); bb[3] = bf16_hi(b23);
+      }
+    }
+    const float y0 = fmaf(v[0] * sa, sb.x, bb[0]), y1 = fmaf(v[1] * sa, sb.y, bb[1]);
+    const float y2 = fmaf(v[2] * sa, sb.z, bb[2]), y3 = fmaf(v[3] * sa, sb.w, bb[3]);
+    *reinterpret_cast<uint2*>(otile + ml * OP + nl * 2) = make_uint2(pack_bf16(y0, y1), pack_bf16(y2, y3));
+  };
+  if constexpr (WK > 1) {
+    // wave w's partial tile into stage w, then every thread sums four partials
+    float* red = reinterpret_cast<float*>(wave == 0 ? st0 : wave == 1 ? st1 : wave == 2 ? st2 : st3);
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[((i * FM + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+    __syncthreads();
+    const float* parts[4] = {reinterpret_cast<const float*>(st0), reinterpret_cast<const float*>(st1),
+                             reinterpret_cast<const float*>(st2), reinterpret_cast<const float*>(st3)};
+#pragma unroll
+    for (int g = tid; g < FN * FM * 4 * 64; g += 256) {
+      const int blk = g >> 8, rq = (g >> 6) & 3, ln = g & 63;
+      const int i = blk / FM, j = blk % FM;
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += parts[w][(blk * 16 + 4 * rq + e) * 64 + ln];
+      final_store(j * 32 + (ln & 31), i * 32 + 8 * rq + 4 * (ln >> 5), v);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          final_store(wm * TM + j * 32 + fr, i * 32 + 8 * q + 4 * fk, v);
+        }
+  }
+  __syncthreads();
+  constexpr int OCR = NP / 8;  // 16-byte chunks per output row
+  for (int g = tid; g < MT * OCR; g += 256) {
+    const int ml = g / OCR, cc = g % OCR;
+    if (ml < mrows && cc * 8 < nrows)
+      stg16(C + (int64_t)(m0 + ml) * ldc + n0 + cc * 8, *reinterpret_cast<const uint4*>(otile + ml * OP + cc * 16));
+  }
+}
+
 struct TileCfg {
   int bm, bn, bk;  // skinny configurations: bm = the largest M they take
   bool skinny;
+  bool stream;  // fp16 a only (stream_kernel); bm = rows of a per block
 };
 // Tiled configurations (block tile, waves, k tile, register sets in flight, LDS stages):
 // 0: 256x256, 8 waves of 64x128 (2 per SIMD), k 32, 3 sets, 3 stages, grouped MFMA schedule
@@ -691,11 +864,15 @@ struct TileCfg {
 // and 12: 128x64, 4 waves of 64x32, k 64, 3 sets, 3 stages
 // Skinny, M <= 32: 13: 64 b rows per block, 8 waves splitting K, 3 chunks in flight
 // Skinny, M <= 64: 14: 64 b rows per block, 8 waves splitting K, 1 chunk in flight
+// Decode on fp16 a (stream_kernel, b rows spread over every CU, direct-to-LDS ring):
+// 15: 32 rows of a, 12 stages; 16: 64 rows, 9 stages; 17: 128 rows, 6 stages;
+// 18: 256 rows, 3 stages
 constexpr TileCfg kCfgs[] = {{256, 256, 32}, {128, 128, 64}, {64, 64, 64},       {128, 128, 64},    {256, 256, 32},
                              {32, 32, 64, true}, {32, 32, 64, true}, {64, 32, 64, true}, {64, 64, 64, true},
                              {256, 256, 64}, {256, 128, 64}, {256, 64, 64}, {128, 64, 64}, {32, 64, 64, true},
-                             {64, 64, 64, true}};
-constexpr int kNumCfgs = 15;
+                             {64, 64, 64, true}, {32, 64, 64, false, true}, {64, 64, 64, false, true},
+                             {128, 64, 64, false, true}, {256, 64, 64, false, true}};
+constexpr int kNumCfgs = 19;
 
 // Compute units of the current device (cached per device).
 int64_t num_cus() {
@@ -710,7 +887,8 @@ int64_t num_cus() {
   return cache[dev];
 }
 
-// Configuration choice, fitted to measurements on MI355X (256 CUs): for M <= 64
+// Configuration choice, fitted to measurements on MI355X (256 CUs). f16a: the caller
+// can supply fp16 a (the decode configurations need it). Otherwise, for M <= 64
 // with enough b rows for 160 blocks, the 64-row skinny block (8 waves splitting
 // K, 3 chunks in flight: 17.6 -> 16.4 us at M = 16, K = 2560, N = 10240) up to M = 32 and
 // the LDS-staged 64x64 tile above (every skinny block re-reads all of a, which
@@ -718,7 +896,12 @@ int64_t num_cus() {
 // eff x (blocks / whole rounds of 256 blocks) x (M / M rounded up to the tile):
 // larger tiles run faster per CU (eff), but a partial last round of blocks or a
 // mostly empty row of tiles wastes CUs.
-int pick_cfg(int64_t M, int64_t N) {
+int pick_cfg(int64_t M, int64_t N, bool f16a) {
+  // decode on fp16 a (a16 given, or tbf16_linear's workspace copy): the direct-to-LDS
+  // ring for M <= 128 once N fills every CU with at least 32 b rows (M = 16 / 64 /
+  // 128 at K = 2560, N = 10240: 13.3 / 18.2 / 23.0 us against 13.6 / 24.1 / 26.9 for
+  // the kernels below; at M = 255 the two tie, and the 256-row tiles skip the copy)
+  if (f16a && M <= 128 && N >= 32 * num_cus()) return M <= 32 ? 15 : M <= 64 ? 16 : 17;
   if (M <= 64) {
     if (cdiv(N, 64) >= 160) return M <= 32 ? 13 : 2;
     return M <= 32 ? 6 : 7;
@@ -760,17 +943,18 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
                 int64_t K, hipStream_t st) {
   const int bm = kCfgs[cfg].bm, bn = kCfgs[cfg].bn;
   TB_CHECK(!kCfgs[cfg].skinny || M <= bm, "gemm: configuration %d takes M <= %d", cfg, bm);
-  // skinny blocks take `rows` weight rows each: as many as fit (bn) when that
-  // already fills whole rounds of blocks over the CUs, else fewer, so that the
-  // weight stream is spread over every CU in as few rounds as possible
+  TB_CHECK(!kCfgs[cfg].stream || !A_BF16, "gemm: configuration %d needs fp16 a (tbf16_gemm_f16 or tbf16_linear)", cfg);
+  // skinny and stream blocks take `rows` weight rows each: as many as fit (bn)
+  // when that already fills whole rounds of blocks over the CUs, else fewer, so
+  // that the weight stream is spread over every CU in as few rounds as possible
   int rows = bn;
-  if (kCfgs[cfg].skinny) {
+  if (kCfgs[cfg].skinny || kCfgs[cfg].stream) {
     const int64_t ncu = num_cus();
     const int64_t rounds = cdiv(cdiv(N, bn), ncu);
     rows = (int)std::min<int64_t>(bn, std::max<int64_t>(8, cdiv(cdiv(N, rounds * ncu), 8) * 8));
   }
-  const int64_t blocks = kCfgs[cfg].skinny ? cdiv(N, rows) : cdiv(M, bm) * cdiv(N, bn);
-  TB_CHECK(blocks < (int64_t)1 << 31, "gemm: grid too large");
+  const int64_t blocks = kCfgs[cfg].skinny || kCfgs[cfg].stream ? cdiv(N, rows) : cdiv(M, bm) * cdiv(N, bn);
+  TB_CHECK(blocks < (int64_t)1 << 31 && cdiv(M, bm) < 65536, "gemm: grid too large");
   const bool even = K % kCfgs[cfg].bk == 0;  // no k-tail selects on loaded values
   const auto a = (const uint16_t*)A;
   const auto b = (const uint16_t*)B;
@@ -797,7 +981,16 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
     case 7: SKINNY(1, 2, 4, 3, true); break;
     case 13: SKINNY(2, 1, 8, 3, true); break;
     case 14: SKINNY(2, 2, 8, 1, true); break;
+#define STREAM(MT_, S_)                                                                                  \
+  if constexpr (!A_BF16)                                                                                 \
+    stream_kernel<MT_, S_><<<dim3(g, (unsigned)cdiv(M, MT_)), 256, 0, st>>>(a, lda, a_sinv, b, ldb, b_sinv, bi, c, \
+                                                                          ldc, M, N, K, rows)
+    case 15: STREAM(32, 12); break;
+    case 16: STREAM(64, 9); break;
+    case 17: STREAM(128, 6); break;
+    case 18: STREAM(256, 3); break;
     default: SKINNY(2, 2, 4, 2, true); break;
+#undef STREAM
 #undef SKINNY
 #undef CFG
   }
@@ -824,37 +1017,79 @@ int check_gemm(const char* fn, int64_t M, int64_t N, int64_t K, const void* A, i
 namespace tbf16 {
 int launch_row_exps(const void* x, int64_t M, int64_t K, int64_t ldx, int t, int l1, int32_t* exps, float* s_inv,
                     hipStream_t st);
+int launch_quantize_rows(const void* x, int64_t R, int64_t K, int64_t ldx, int t, int l1, void* y16, int64_t ldy,
+                         float* s_inv, int32_t* exps, hipStream_t st);
+}  // namespace tbf16
+
+namespace {
+
+// Workspace of tbf16_linear: the row exponents (int32 (M,)) and, where the chosen
+// configuration takes fp16 a (the decode kernel), the row inverse scales (fp32
+// (M,)) and the scaled fp16 copy of x (M, K), each 256-byte aligned.
+struct LinearWs {
+  size_t exps, sinv, x16, bytes;
+};
+LinearWs linear_ws(int64_t M, int64_t K, int cfg) {
+  LinearWs w{0, 0, 0, align_up((size_t)M * 4, 256)};
+  if (cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg].stream) {
+    w.sinv = w.bytes;
+    w.x16 = w.sinv + align_up((size_t)M * 4, 256);
+    w.bytes = w.x16 + (size_t)M * (size_t)K * 2;
+  }
+  return w;
+}
+
+int linear_into(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N, int64_t ldw,
+                const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg, uint8_t* wsp,
+                hipStream_t st) {
+  const LinearWs w = linear_ws(M, K, cfg);
+  int32_t* exps = reinterpret_cast<int32_t*>(wsp + w.exps);
+  if (!kCfgs[cfg].stream) {
+    if (int rc = launch_row_exps(x, M, K, ldx, t, l1, exps, nullptr, st)) return rc;
+    return launch_gemm<true>(cfg, x, ldx, exps, nullptr, w16, ldw, ws, bias, y, ldy, M, N, K, st);
+  }
+  // decode: x quantised once (exponents, inverse scales, fp16 rows), then the GEMM
+  // on fp16 operands; the same fp16 values the fused kernels convert in registers
+  float* sinv = reinterpret_cast<float*>(wsp + w.sinv);
+  void* x16 = wsp + w.x16;
+  if (int rc = launch_quantize_rows(x, M, K, ldx, t, l1, x16, K, sinv, exps, st)) return rc;
+  return launch_gemm<false>(cfg, x16, K, nullptr, sinv, w16, ldw, ws, bias, y, ldy, M, N, K, st);
+}
+}  // namespace
+
+extern "C" size_t tbf16_linear_ws_bytes(int64_t M, int64_t K, int64_t N, int cfg) {
+  if (M <= 0 || K < 0 || N <= 0 || cfg >= kNumCfgs) return M > 0 ? (size_t)M * 4 : 0;
+  return linear_ws(M, K, cfg < 0 ? pick_cfg(M, N, true) : cfg).bytes;
 }
 
 extern "C" int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N,
                             int64_t ldw, const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1,
-                            int cfg, int32_t* exps_ws, void* stream) {
+                            int cfg, void* workspace, void* stream) {
   if (int rc = check_gemm("linear", M, N, K, x, ldx, w16, ldw, ws, bias, y, ldy)) return rc;
-  TB_CHECK(exps_ws != nullptr || M == 0, "linear: exps workspace missing");
+  TB_CHECK(workspace != nullptr || M == 0, "linear: workspace missing");
+  TB_CHECK(aligned16(workspace), "linear: workspace must be 16-byte aligned");
   TB_CHECK(cfg < kNumCfgs, "bad cfg");
   if (M == 0 || N == 0) return 0;
-  hipStream_t st = as_stream(stream);
-  if (int rc = launch_row_exps(x, M, K, ldx, t, l1, exps_ws, nullptr, st)) return rc;
-  return launch_gemm<true>(cfg < 0 ? pick_cfg(M, N) : cfg, x, ldx, exps_ws, nullptr, w16, ldw, ws, bias, y, ldy, M, N,
-                           K, st);
+  return linear_into(x, M, K, ldx, w16, N, ldw, ws, bias, y, ldy, t, l1, cfg < 0 ? pick_cfg(M, N, true) : cfg,
+                     static_cast<uint8_t*>(workspace), as_stream(stream));
 }
 
-// ---- tbf16_linear_noalloc: the row exponents in a static device array ----------
-// Each GPU the library runs on holds one copy of `scratch` (4 MiB) until the process
-// ends. Host code never passes the array's name to a kernel (on the host it is only
-// a stand-in symbol): the device address of this GPU's copy comes from
-// hipGetSymbolAddress, taken once per device with that device current, and is
-// what the kernels get. Every call on one GPU shares the array, and the row pass
-// overwrites exactly the rows a call uses before its GEMM reads them, so nothing
+// ---- tbf16_linear_noalloc: the workspace in a static device array ---------------
+// Each GPU the library runs on holds one copy of `scratch` (TBF16_NOALLOC_SCRATCH_BYTES)
+// until the process ends. Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in symbol): the device address of this GPU's copy
+// comes from hipGetSymbolAddress, taken once per device with that device current,
+// and is what the kernels get. Every call on one GPU shares the array, and the row
+// pass overwrites exactly the part a call uses before its GEMM reads it, so nothing
 // needs clearing; calls that overlap on one GPU (several streams or threads) race.
-static __device__ __align__(256) int32_t scratch[TBF16_NOALLOC_MAX_ROWS];
+static __device__ __align__(256) uint8_t scratch[TBF16_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
-int32_t* g_scratch[kMaxDevices] = {};
+uint8_t* g_scratch[kMaxDevices] = {};
 
-int scratch_ptr(int32_t** out) {
+int scratch_ptr(uint8_t** out) {
   int dev = -1;
   TB_CHECK(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices, "linear_noalloc: no current device");
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -862,7 +1097,7 @@ int scratch_ptr(int32_t** out) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     TB_CHECK(e == hipSuccess && p != nullptr, "linear_noalloc: hipGetSymbolAddress failed (%s)", hipGetErrorString(e));
-    g_scratch[dev] = static_cast<int32_t*>(p);
+    g_scratch[dev] = static_cast<uint8_t*>(p);
   }
   *out = g_scratch[dev];
   return 0;
@@ -877,12 +1112,14 @@ extern "C" int tbf16_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t
   if (int rc = check_gemm("linear_noalloc", M, N, K, x, ldx, w16, ldw, ws, bias, y, ldy)) return rc;
   TB_CHECK(cfg < kNumCfgs, "bad cfg");
   if (M == 0 || N == 0) return 0;
-  int32_t* exps = nullptr;
-  if (int rc = scratch_ptr(&exps)) return rc;
-  hipStream_t st = as_stream(stream);
-  if (int rc = launch_row_exps(x, M, K, ldx, t, l1, exps, nullptr, st)) return rc;
-  return launch_gemm<true>(cfg < 0 ? pick_cfg(M, N) : cfg, x, ldx, exps, nullptr, w16, ldw, ws, bias, y, ldy, M, N, K,
-                           st);
+  const int c = cfg < 0 ? pick_cfg(M, N, true) : cfg;
+  const size_t need = linear_ws(M, K, c).bytes;
+  TB_CHECK(need <= TBF16_NOALLOC_SCRATCH_BYTES,
+           "linear_noalloc: %lld x %lld needs %zu workspace bytes, beyond the scratch limit of %d bytes", (long long)M,
+           (long long)K, need, TBF16_NOALLOC_SCRATCH_BYTES);
+  uint8_t* wsp = nullptr;
+  if (int rc = scratch_ptr(&wsp)) return rc;
+  return linear_into(x, M, K, ldx, w16, N, ldw, ws, bias, y, ldy, t, l1, c, wsp, as_stream(stream));
 }
 
 extern "C" int tbf16_linear_exps(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t* exps,
@@ -892,7 +1129,7 @@ extern "C" int tbf16_linear_exps(const void* x, int64_t M, int64_t K, int64_t ld
   TB_CHECK(exps != nullptr || M == 0, "linear_exps: exps missing");
   TB_CHECK(cfg < kNumCfgs, "bad cfg");
   if (M == 0 || N == 0) return 0;
-  return launch_gemm<true>(cfg < 0 ? pick_cfg(M, N) : cfg, x, ldx, exps, nullptr, w16, ldw, ws, bias, y, ldy, M, N, K,
+  return launch_gemm<true>(cfg < 0 ? pick_cfg(M, N, false) : cfg, x, ldx, exps, nullptr, w16, ldw, ws, bias, y, ldy, M, N, K,
                            as_stream(stream));
 }
 
@@ -903,6 +1140,6 @@ extern "C" int tbf16_gemm_f16(const void* a16, int64_t M, int64_t K, int64_t lda
   TB_CHECK(sa != nullptr || M == 0, "gemm_f16: sa missing");
   TB_CHECK(cfg < kNumCfgs, "bad cfg");
   if (M == 0 || N == 0) return 0;
-  return launch_gemm<false>(cfg < 0 ? pick_cfg(M, N) : cfg, a16, lda, nullptr, sa, b16, ldb, sb, bias, y, ldy, M, N,
+  return launch_gemm<false>(cfg < 0 ? pick_cfg(M, N, true) : cfg, a16, lda, nullptr, sa, b16, ldb, sb, bias, y, ldy, M, N,
                             K, as_stream(stream));
 }

@@ -33,7 +33,8 @@ __global__ __launch_bounds__(256) void row_exps_kernel(const uint16_t* __restric
 // quantize_rows: amax pass, then y = fp16(x * 2^p) (small_kernels.cu:35-74).
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t R, int K,
                                                             int64_t ldx, int t, int l1, uint16_t* __restrict__ y,
-                                                            int64_t ldy, float* __restrict__ s_inv) {
+                                                            int64_t ldy, float* __restrict__ s_inv,
+                                                            int32_t* __restrict__ exps) {
   const int64_t row = (int64_t)blockIdx.x * kRowWaves + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= R) return;
@@ -44,7 +45,10 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __re
   const uint4* src = reinterpret_cast<const uint4*>(xr);
   uint4* dst = reinterpret_cast<uint4*>(y + row * ldy);
   for (int i = lane; i < (K >> 3); i += kWave) dst[i] = cvt_bf16x8_f16x8(src[i], s);
-  if (lane == 0) s_inv[row] = ldexp1(-p);
+  if (lane == 0) {
+    s_inv[row] = ldexp1(-p);
+    if (exps) exps[row] = p;
+  }
 }
 
 // Transposing convert: yT[c][r] = fp16((x[r][c] * rowmul[r]) * colmul[c]). Each
@@ -372,6 +376,16 @@ int launch_row_exps(const void* x, int64_t M, int64_t K, int64_t ldx, int t, int
   TB_LAUNCH_CHECK("row_exps");
   return 0;
 }
+
+// y16 = fp16(x * 2^p[r]), s_inv[r] = 2^-p[r] and, if exps is given, exps[r] = p[r]
+int launch_quantize_rows(const void* x, int64_t R, int64_t K, int64_t ldx, int t, int l1, void* y16, int64_t ldy,
+                         float* s_inv, int32_t* exps, hipStream_t st) {
+  if (R == 0) return 0;
+  quantize_rows_kernel<<<(unsigned)cdiv(R, kRowWaves), 256, 0, st>>>((const uint16_t*)x, R, (int)K, ldx, t, l1,
+                                                                     (uint16_t*)y16, ldy, s_inv, exps);
+  TB_LAUNCH_CHECK("quantize_rows");
+  return 0;
+}
 }  // namespace tbf16
 
 extern "C" int tbf16_row_exps(const void* x, int64_t M, int64_t K, int64_t ldx, int t, int l1, int32_t* exps,
@@ -386,10 +400,7 @@ extern "C" int tbf16_quantize_rows(const void* x, int64_t R, int64_t K, int64_t 
   if (int rc = check_rows("quantize_rows", x, R, K, ldx)) return rc;
   TB_CHECK(ldy % 8 == 0 && ldy >= K && aligned16(y16) && s_inv, "quantize_rows: bad output");
   if (R == 0) return 0;
-  quantize_rows_kernel<<<(unsigned)cdiv(R, kRowWaves), 256, 0, as_stream(stream)>>>(
-      (const uint16_t*)x, R, (int)K, ldx, t, l1, (uint16_t*)y16, ldy, s_inv);
-  TB_LAUNCH_CHECK("quantize_rows");
-  return 0;
+  return launch_quantize_rows(x, R, K, ldx, t, l1, y16, ldy, s_inv, nullptr, as_stream(stream));
 }
 
 extern "C" int tbf16_quantize_rows_t(const void* x, int64_t R, int64_t K, int64_t ldx, int t, void* yT, int64_t ldyT,

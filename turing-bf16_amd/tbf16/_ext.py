@@ -14,7 +14,7 @@ import pathlib
 import torch
 
 _LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libtbf16_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DT_BF16, DT_F16 = 0, 1
 
@@ -38,6 +38,7 @@ _SIGS = {
     "tbf16_quantize_rows_t": (I, [P, I64, I64, I64, I, P, I64, P, P, P]),
     "tbf16_quantize_cols_ws_bytes": (SZ, [I64, I64]),
     "tbf16_quantize_cols_t": (I, [P, I64, I64, I64, I, P, P, I64, P, P, I64, P]),
+    "tbf16_linear_ws_bytes": (SZ, [I64, I64, I64, I]),
     "tbf16_linear": (I, [P, I64, I64, I64, P, I64, I64, P, P, P, I64, I, I, I, P, P]),
     "tbf16_linear_noalloc": (I, [P, I64, I64, I64, P, I64, I64, P, P, P, I64, I, I, I, P]),
     "tbf16_linear_exps": (I, [P, I64, I64, I64, P, P, I64, I64, P, P, P, I64, I, P]),

@@ -18,7 +18,7 @@ import torch
 import torch.nn.functional as F
 
 from . import routing
-from ._ext import available, launch, ptr  # noqa: F401  (available re-exported as in the reference)
+from ._ext import available, launch, lib, ptr  # noqa: F401  (available re-exported as in the reference)
 
 # TBF16_GEMM=fused forces the max-scaled fused path for every M >= 2 (the reference's
 # switch between its fused kernel and the cuBLAS path, tbf16/ops.py:20-23). Unset:
@@ -137,9 +137,10 @@ def _linear(x2, w16, w_sinv, bias, t, l1):
     x2, w16, ws, b, N, Np = _prep_gemm_operands(x2, w16, w_sinv, bias)
     M, Kp = x2.shape
     y = torch.empty((M, Np), device=x2.device, dtype=torch.bfloat16)
-    exps = torch.empty((M,), device=x2.device, dtype=torch.int32)
+    wsb = int(lib().tbf16_linear_ws_bytes(M, Kp, Np, _GEMM_CFG))
+    work = torch.empty((wsb,), device=x2.device, dtype=torch.uint8)
     launch("tbf16_linear", x2, ptr(x2), M, Kp, x2.stride(0), ptr(w16), Np, w16.stride(0), ptr(ws), ptr(b), ptr(y),
-           y.stride(0), int(t), int(l1), _GEMM_CFG, ptr(exps))
+           y.stride(0), int(t), int(l1), _GEMM_CFG, ptr(work))
     return y if Np == N else y[:, :N]
 
 
