@@ -42,9 +42,11 @@ def _no_alloc(x, w16, ws, b, t, l1):
 
 
 def test_noalloc_matches_workspace_entry_point(dev):
-    # first call: 4096 rows (the fused max-scaled path); second, smaller: 200 rows with
-    # L1 row scales (the decode path), whose exponents overwrite the first call's
-    for (M, K, N, t, l1, seed) in ((4096, 2048, 1024, 15, 0, 1), (200, 2560, 768, 15, 1, 2)):
+    # first call: 4096 rows (the fused max-scaled path); then, smaller, 200 rows with L1
+    # row scales (256-row tiles) and 64 rows against N = 10240 (the decode kernel, its
+    # fp16 copy of x in the scratch array), each overwriting the previous call's
+    for (M, K, N, t, l1, seed) in ((4096, 2048, 1024, 15, 0, 1), (200, 2560, 768, 15, 1, 2),
+                                   (64, 2560, 10240, 15, 1, 3)):
         x, w16, ws, b = _inputs(dev, M, K, N, seed)
         want = _with_workspace(x, w16, ws, b, t, l1)
         got = _no_alloc(x, w16, ws, b, t, l1)
