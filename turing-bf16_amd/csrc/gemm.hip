@@ -73,15 +73,16 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   static_assert(FM >= 1 && FN >= 1 && AL * RP == BM && BL * RP == BN, "bad tile");
   constexpr int RB = BK * 2;  // bytes per LDS tile row
   constexpr int STAGE = (BM + BN) * RB;
-  // epilogue staging: tile rows of PITCH bytes, in passes of RPP rows (>= one wave's rows)
-  constexpr int PITCH = BN * 2 + 16;
-  constexpr int PFIT = (BM * PITCH <= 2 * STAGE) ? 1 : (BM / 2 * PITCH <= 2 * STAGE) ? 2 : 4;
-  constexpr int PASSES = PFIT < BM / TM ? PFIT : BM / TM;
-  constexpr int RPP = BM / PASSES;
   constexpr int NSTG = NS == 5 ? 2 : NS >= 3 ? 3 : 2;  // LDS stages
   constexpr bool SCHED = NS == 4;
-  constexpr int SMEM = NSTG * STAGE > RPP * PITCH ? NSTG * STAGE : RPP * PITCH;
+  // after the stages: the epilogue's factors for the tile, sa[BM] and sb[BN] (fp32)
+  // and bias[BN] (bf16), written once before the first barrier
+  constexpr int SMEM = NSTG * STAGE + (BM + BN) * 4 + BN * 2;
+  static_assert(SMEM <= 160 * 1024, "LDS");
   __shared__ __align__(16) uint8_t smem[SMEM];
+  float* const sa_l = reinterpret_cast<float*>(smem + NSTG * STAGE);
+  float* const sb_l = sa_l + BM;
+  uint16_t* const bias_l = reinterpret_cast<uint16_t*>(sb_l + BN);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -96,6 +97,21 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   const int within = bid % (GM * tiles_n);
   const int m0 = (first + within % gsize) * BM;
   const int n0 = (within / gsize) * BN;
+
+  // the epilogue's factors (rows past M / columns past N get 0 and are not stored)
+  for (int t = tid; t < BM; t += NT) {
+    float s = 0.f;
+    if (m0 + t < M) {
+      if constexpr (A_BF16) s = ldexp1(-a_exp[m0 + t]);
+      else s = a_sinv[m0 + t];
+    }
+    sa_l[t] = s;
+  }
+  for (int t = tid; t < BN; t += NT) {
+    const bool ok = n0 + t < N;
+    sb_l[t] = ok ? b_sinv[n0 + t] : 0.f;
+    bias_l[t] = ok && bias ? bias[n0 + t] : (uint16_t)0;
+  }
 
   // ---- global -> register staging through buffer loads ----
   // One buffer resource per operand tile (SGPRs), loop-invariant 32-bit row
@@ -418,56 +434,43 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
     }
   }
 
-  // ---- epilogue: (acc * sa[m]) * sb[n] + bias[n] -> bf16, staged through LDS so
-  // that each row of the tile leaves as whole 16-byte-per-lane runs ----
+  // ---- epilogue: (acc * sa[m]) * sb[n] + bias[n] -> bf16 straight from registers ----
+  // Lane l holds columns 8 q + 4 (l / 32) .. + 3 of row l % 32 for q = 0..3; one
+  // v_permlane32_swap per dword pairs q = 2p (kept by lanes < 32) with q = 2p + 1
+  // (kept by lanes >= 32), so every lane stores 8 consecutive columns (16 bytes)
+  // and no LDS round trip or barrier is needed.
 #pragma unroll
-  for (int pass = 0; pass < PASSES; ++pass) {
-    if (wm * TM / RPP == pass) {
+  for (int j = 0; j < FM; ++j) {
+    const int ml = wm * TM + j * 32 + fr;  // row within the tile
+    const float sa = sa_l[ml];
+    const bool mok = m0 + ml < M;
 #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const int ml = wm * TM + j * 32 + fr;  // row within the tile
-        const int m = m0 + ml;
-        float sa = 0.f;
-        if (m < M) {
-          if constexpr (A_BF16) sa = ldexp1(-a_exp[m]);
-          else sa = a_sinv[m];
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        uint32_t w[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int q = 2 * p + h;
+          const int nl = wn * TN + i * 32 + 8 * q + 4 * fk;
+          const float4 sb = *reinterpret_cast<const float4*>(sb_l + nl);
+          const uint2 bw = *reinterpret_cast<const uint2*>(bias_l + nl);
+          const float y0 = fmaf(acc[i][j][4 * q + 0] * sa, sb.x, bf16_lo(bw.x));
+          const float y1 = fmaf(acc[i][j][4 * q + 1] * sa, sb.y, bf16_hi(bw.x));
+          const float y2 = fmaf(acc[i][j][4 * q + 2] * sa, sb.z, bf16_lo(bw.y));
+          const float y3 = fmaf(acc[i][j][4 * q + 3] * sa, sb.w, bf16_hi(bw.y));
+          w[h][0] = pack_bf16(y0, y1);
+          w[h][1] = pack_bf16(y2, y3);
         }
-        uint8_t* srow = smem + (ml - pass * RPP) * PITCH;
-#pragma unroll
-        for (int i = 0; i < FN; ++i) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int nl = wn * TN + i * 32 + 8 * q + 4 * fk;
-            const int n = n0 + nl;
-            float4 sb = make_float4(0.f, 0.f, 0.f, 0.f);
-            float bb[4] = {0.f, 0.f, 0.f, 0.f};
-            if (n < N) {
-              sb = *reinterpret_cast<const float4*>(b_sinv + n);
-              if (bias) {
-                const uint32_t b01 = *reinterpret_cast<const uint32_t*>(bias + n);
-                const uint32_t b23 = *reinterpret_cast<const uint32_t*>(bias + n + 2);
-                bb[0] = bf16_lo(b01); bb[1] = bf16_hi(b01); bb[2] = bf16_lo(b23); bb[3] = bf16_hi(b23);
-              }
-            }
-            const float y0 = fmaf(acc[i][j][4 * q + 0] * sa, sb.x, bb[0]);
-            const float y1 = fmaf(acc[i][j][4 * q + 1] * sa, sb.y, bb[1]);
-            const float y2 = fmaf(acc[i][j][4 * q + 2] * sa, sb.z, bb[2]);
-            const float y3 = fmaf(acc[i][j][4 * q + 3] * sa, sb.w, bb[3]);
-            *reinterpret_cast<uint2*>(srow + nl * 2) = make_uint2(pack_bf16(y0, y1), pack_bf16(y2, y3));
-          }
-        }
+        // [0]: lanes < 32 keep their own q = 2p dword, lanes >= 32 receive lane
+        // l - 32's q = 2p + 1 dword; [1]: lanes < 32 receive lane l + 32's q = 2p
+        // dword, lanes >= 32 keep their own q = 2p + 1 dword
+        const auto d0 = __builtin_amdgcn_permlane32_swap(w[0][0], w[1][0], false, false);
+        const auto d1 = __builtin_amdgcn_permlane32_swap(w[0][1], w[1][1], false, false);
+        const int n = n0 + wn * TN + i * 32 + 16 * p + 8 * fk;
+        if (mok && n < N) stg16(C + (int64_t)(m0 + ml) * ldc + n, make_uint4(d0[0], d1[0], d0[1], d1[1]));
       }
     }
-    __syncthreads();
-    constexpr int OCR = BN / 8;  // 16-byte chunks per output tile row
-#pragma unroll
-    for (int c = tid; c < RPP * OCR; c += NT) {
-      const int rl = c / OCR, cc = c % OCR;
-      const int m = m0 + pass * RPP + rl, n = n0 + cc * 8;
-      if (m < M && n < N)
-        stg16(C + (int64_t)m * ldc + n, *reinterpret_cast<const uint4*>(smem + rl * PITCH + cc * 16));
-    }
-    if (PASSES > 1) __syncthreads();
   }
 }
 
