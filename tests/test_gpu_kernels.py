@@ -107,7 +107,7 @@ def test_quantize_rows_t_and_cols_t_bit_exact(dev):
 
 # tiled configurations take any M; skinny ones (5-8, 13, 14) M <= 32 or 64; the
 # decode ones (15-18, fp16 a) any M, in row tiles of 32 / 64 / 128 / 256
-GEMM_CFG_M = {0: 300, 1: 300, 2: 300, 3: 300, 4: 300, 5: 29, 6: 29, 7: 61, 8: 61, 9: 300, 10: 300, 11: 300, 12: 300,
+GEMM_CFG_M = {0: 300, 1: 300, 2: 300, 3: 300, 4: 300, 5: 29, 6: 29, 7: 61, 8: 61, 9: 300, 10: 300, 11: 300, 12: 300, 19: 300,
               13: 29, 14: 61, 15: 300, 16: 300, 17: 300, 18: 300}
 STREAM_CFGS = (15, 16, 17, 18)
 
