@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TBF16_ABI_VERSION 2
+#define TBF16_ABI_VERSION 3
 
 #define TBF16_OK 0
 #define TBF16_EINVAL (-1) /* bad shape, stride, alignment or dtype */
@@ -184,10 +184,16 @@ int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64
  * e = max(frexp(amax dout[b,h]) + ev_q[b,h]), G = t_do - e, dO16 = fp16(dout *
  * 2^(ev_q + G)). dq = bf16(scale * dS K16 * 2^(a-G)), dk = bf16(scale * sum_grp
  * dS^T Q16 * 2^(-a-G)), dv = bf16(sum_grp P^T dO16 * 2^(-ev-G)), all from fp32.
- * *overflow is set to 1 (device int, caller zeroes it) when any gradient in the
- * scaled fp16 domain would overflow fp16 (|x| >= 65520) or is not finite, which
- * is the reference's retry condition (tbf16/autograd.py:177-189). exps_out int32
- * [2] = {e, G}. Inputs are the forward's q, k, v, o16, lse and exps; same shape
+ * *overflow (device int32) receives the bit pattern of the largest magnitude of
+ * the gradients in the scaled fp16 domain (dq16, dk16, dv16; +inf if any is not
+ * finite); at 65520 and above (bits >= 0x477FF000) they would overflow fp16, the
+ * reference's retry condition (tbf16/autograd.py:177-189). exps_out int32 [2] =
+ * {e, G}. gate: null, or the overflow word of an earlier call with the same
+ * arguments and workspace. A gated call is the reference's retry loop run on the
+ * device: it does nothing when that call's maximum was below 65520, else it runs
+ * at t_do - 8 r with r the number of retries the reference would take (each
+ * retry scales every value by 2^-8, at most 5), writing the same outputs and its
+ * own overflow word; no host round trip is needed between the two calls. Inputs are the forward's q, k, v, o16, lse and exps; same shape
  * rules as the forward (D % 8 == 0, D <= 256); dropout_p and seed as given to
  * the forward (its mask is regenerated: dV from P o Z, dS = P o (Z o dP - delta)
  * with Z = keep / (1 - p)).
@@ -199,8 +205,8 @@ int tbf16_attn_bwd(const void* q, const void* k, const void* v, const void* o16,
                    int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
                    const int64_t* v_strides, const int64_t* do_strides, const void* bias,
                    const int64_t* bias_strides, float scale, int causal, int t_do, float dropout_p, uint64_t seed,
-                   void* dq, void* dk, void* dv, int32_t* exps_out, int32_t* overflow, void* ws, int64_t ws_bytes,
-                   void* stream);
+                   void* dq, void* dk, void* dv, int32_t* exps_out, int32_t* overflow, const int32_t* gate,
+                   void* ws, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

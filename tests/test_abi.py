@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _ext.lib().tbf16_abi_version() == _ext.ABI_VERSION == 2
+    assert _ext.lib().tbf16_abi_version() == _ext.ABI_VERSION == 3
 
 
 def _err():
@@ -67,7 +67,7 @@ def test_host_validation_rejects_before_launch():
     assert "dropout_p" in _err()
     # backward head dim limit
     assert L.tbf16_attn_bwd(16, 16, 16, 16, 16, 16, 16, 1, 2, 2, 8, 8, 264, st, st, st, st, None, None, 1.0, 0, 5, 0.0, 0,
-                            16, 16, 16, 16, 16, 16, 1 << 20, None) == -1
+                            16, 16, 16, 16, 16, None, 16, 1 << 20, None) == -1
     # convolution passes: misaligned input, small workspace, null epilogue operand
     assert L.tbf16_conv_input(18, 2, 64, 0, 16, 16, 16, 1 << 10, None) == -1
     assert "aligned" in _err()

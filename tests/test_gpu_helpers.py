@@ -277,3 +277,55 @@ def test_sdpa_dropout_near_one(dev):
                                      seed=seed)
     for n, a, r in (("dq", dq, qd.grad), ("dk", dk, kd.grad), ("dv", dv, vd.grad)):
         assert torch.isfinite(a).all() and rel(a, r) < 3e-3, (n, rel(a, r))
+
+
+def _dominant_key_case(dev, S, D=64):
+    """Key 0 takes 99.2% of every query's attention (logit 12.5 against 0) and dO is
+    constant, so dO16 = 2^(t_do - 1) = 32 everywhere and dv16 of key 0 is about
+    S * 0.992 * 32: past 65520 at S = 4096 (the reference retries once, t_do - 8),
+    8127 at S = 256 (no retry)."""
+    q = torch.zeros(1, 1, S, D)
+    q[..., 0] = 10.0
+    k = torch.zeros(1, 1, S, D)
+    k[0, 0, 0, 0] = 10.0
+    v = torch.randn(1, 1, S, D, generator=G(31))
+    do = torch.ones(1, 1, S, D)
+    return tuple(t.bfloat16().to(dev) for t in (q, k, v, do))
+
+
+@pytest.mark.parametrize("overflowing", [True, False])
+def test_attn_backward_device_retry_matches_host_loop(dev, overflowing):
+    """The default backward decides the overflow retry on the device (a gated second
+    call); its gradients and {e, G} equal, bit for bit, those of the reference's host
+    loop (check='sync'), in a case that retries once and in one that does not."""
+    q, k, v, do = _dominant_key_case(dev, 4096 if overflowing else 256)
+    D = q.shape[-1]
+    sc = 1 / math.sqrt(D)
+    o, lse, o16, exps = attention.attn_forward(q, k, v, None, False, sc, 0, True, True)
+    host = ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="sync")
+    devc = ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="device")
+    ag.check_pending(block=True)
+    t_do = 12 - math.ceil(math.log2(D))
+    e = int(host[3][0])
+    assert int(host[3][1]) == t_do - e - (8 if overflowing else 0)
+    assert torch.equal(host[3].cpu(), devc[3].cpu())
+    for n, a, b in zip(("dq", "dk", "dv"), host[:3], devc[:3]):
+        assert torch.isfinite(a).all() and np.array_equal(bits(a), bits(b)), n
+    # dv (the gradient that overflowed) against fp64 autograd
+    qd, kd, vd = (t.double().requires_grad_() for t in (q, k, v))
+    (torch.softmax(qd @ kd.transpose(-1, -2) * sc, -1) @ vd).backward(do.double())
+    assert rel(devc[2], vd.grad) < 3e-3, rel(devc[2], vd.grad)
+
+
+def test_attn_backward_device_retry_reports_persistent_overflow(dev):
+    """A non-finite dO overflows every retry: the device-mode backward returns, and
+    the deferred check raises FloatingPointError as the host loop does at once."""
+    q, k, v, do = _dominant_key_case(dev, 256)
+    do[0, 0, 3, 5] = float("inf")
+    sc = 1 / 8
+    o, lse, o16, exps = attention.attn_forward(q, k, v, None, False, sc, 0, True, True)
+    with pytest.raises(FloatingPointError):
+        ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="sync")
+    ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="device")
+    with pytest.raises(FloatingPointError):
+        ag.check_pending(block=True)

@@ -27,7 +27,9 @@ class _Fake:
         self.t_dos.append(t_do)
         bad = len(self.t_dos) <= self.n_bad
         z = torch.zeros(1)
-        return z, z, z, torch.zeros(2, dtype=torch.int32), torch.tensor([1 if bad else 0], dtype=torch.int32)
+        # overflow word: float bits of the largest fp16 intermediate (+inf when overflowing)
+        return z, z, z, torch.zeros(2, dtype=torch.int32), torch.tensor([0x7F800000 if bad else 0x46000000],
+                                                                       dtype=torch.int32)
 
 
 def _q(D):
@@ -58,6 +60,44 @@ def test_check_disabled_runs_once():
     f = _Fake(100)
     autograd.attn_backward(_q(128), None, None, None, None, None, None, None, 1.0, False, check=False, attempt_fn=f)
     assert f.t_dos == [5]
+
+
+class _Done:
+    """A finished CUDA event, for the deferred check of device-mode backwards."""
+
+    def query(self):
+        return True
+
+    def synchronize(self):
+        pass
+
+
+class _Busy(_Done):
+    def query(self):
+        return False
+
+
+def test_overflow_word_threshold():
+    # 65504 (fp16 max) and 65519.99 round to finite fp16; 65520 and above do not
+    for x, bad in ((65504.0, False), (65519.99, False), (65520.0, True), (1e30, True), (float("inf"), True),
+                   (float("nan"), True), (0.0, False)):
+        word = torch.tensor([x], dtype=torch.float32).view(torch.int32).abs()[0] if x == x else 0x7FC00000
+        assert autograd._overflowed(int(word)) == bad, x
+
+
+def test_deferred_check_raises_only_for_a_persistent_overflow():
+    ok, inf, big = 0x46000000, 0x7F800000, 0x47800000  # 8192, +inf, 65536
+    autograd._pending[:] = [(_Done(), torch.tensor([ok, inf], dtype=torch.int32)),   # retry not run: word 2 unused
+                            (_Done(), torch.tensor([big, ok], dtype=torch.int32))]   # the retry fixed it
+    autograd.check_pending()
+    assert autograd._pending == []
+    busy = (_Busy(), torch.tensor([inf, inf], dtype=torch.int32))
+    autograd._pending[:] = [busy]
+    autograd.check_pending()  # not finished: left for later, no error yet
+    assert autograd._pending == [busy]
+    with pytest.raises(FloatingPointError):
+        autograd.check_pending(block=True)
+    assert autograd._pending == []
 
 
 def test_target_exp_matches_oracle():

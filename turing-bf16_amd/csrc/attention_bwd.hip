@@ -10,9 +10,14 @@
 //   dv = bf16(sum_q P^T dO16 * 2^(-ev-G)), dk = bf16(scale * sum_q dS^T Q16 * 2^(-a-G)),
 //   dq = bf16(scale * sum_k dS K16 * 2^(a-G)), each from fp32 accumulators.
 // The fp16 values the reference's kernel would round its gradients to are
-// scale * dS K16 (dq16), scale * dS^T Q16 (dk16) and P^T dO16 (dv16): if any of them
-// reaches 65520 or is not finite the overflow flag is raised and the caller retries
-// with t_do - 8 (the reference's condition, tbf16/autograd.py:184-187).
+// scale * dS K16 (dq16), scale * dS^T Q16 (dk16) and P^T dO16 (dv16): the largest of
+// their magnitudes goes to the `overflow` word (float bits, +inf if any is not
+// finite); at 65520 and above the reference retries with t_do - 8
+// (tbf16/autograd.py:184-187). A launch given a `gate` (the word of an earlier
+// attempt at the same t_do) runs only if that attempt overflowed, at t_do - 8 r with
+// r the retries the reference would take: all values scale by exactly 2^-8 per
+// retry, so r follows from the earlier maximum. Every kernel of a gated launch
+// returns at once when r = 0, so the retry needs no host round trip.
 //
 // Kernels (4 waves, v_mfma_f32_32x32x16_f16):
 //   prep:    q16, k16, v16 (one launch, memory-bound); its first block derives e, G.
@@ -66,7 +71,8 @@ struct BwdParams {
   uint16_t *q16, *k16, *v16, *do16;
   int Sqp, Skp, DPc;
   int32_t* exps_out;  // {e, G}
-  int32_t* overflow;
+  int32_t* overflow;      // largest fp16 intermediate magnitude (float bits), this attempt
+  const int32_t* gate;    // null, or an earlier attempt's `overflow` word (see above)
   uint16_t *dq, *dk, *dv;
   // dropout of the forward pass (DROP kernels regenerate its keep mask)
   uint32_t drop_lo, drop_hi, drop_thr;
@@ -110,19 +116,44 @@ __device__ int compute_e(const BwdParams& p, int* red) {
   return max(max(red[0], red[1]), max(red[2], red[3]));
 }
 
-__device__ __forceinline__ bool bad16(float x) { return !(fabsf(x) < kF16Overflow); }
+// Retries the reference takes after an attempt whose largest fp16 intermediate had
+// magnitude x (the bits of a non-negative float, +inf / NaN when not finite): the
+// first r with x 2^(-8 r) < 65520, at most kAttnRetries - 1.
+constexpr int kAttnRetries = 6;
+__device__ __forceinline__ int retries_after(int32_t bits) {
+  float x = __int_as_float(bits);
+  int r = 0;
+  while (r < kAttnRetries - 1 && !(x < kF16Overflow)) {
+    x *= 0x1p-8f;
+    ++r;
+  }
+  return r;
+}
+// a gated launch whose gate needs no retry does nothing
+__device__ __forceinline__ bool gated_off(const BwdParams& p) { return p.gate && retries_after(*p.gate) == 0; }
+// Largest |x| seen by the wave (non-finite as +inf) into the attempt's overflow word:
+// float bits of non-negative values order as integers.
+__device__ __forceinline__ void record_max(const BwdParams& p, float mx, bool nonfinite) {
+  int bits = nonfinite ? 0x7f800000 : __float_as_int(mx);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) bits = max(bits, __shfl_xor(bits, o, 64));
+  if ((threadIdx.x & 63) == 0 && bits > 0) atomicMax(p.overflow, bits);
+}
 
 // ---- q16 = fp16(q 2^a), k16 = fp16(k 2^-a), v16 = fp16(v 2^-ev), and {e, G} -----
 // Grid: x = groups of 4 x 256 / (DP / 8) padded rows, y = (copy, batch, head) with the
 // q heads first, then the k and v heads. Zeros past the real rows and columns.
 // Block (0, 0) also derives e and G (they are needed by the delta pass only).
 __global__ __launch_bounds__(NTH) void prep_kernel(BwdParams p) {
+  if (gated_off(p)) return;
   __shared__ int red[4];
   if (blockIdx.x == 0 && blockIdx.y == 0) {
     const int e = compute_e(p, red);
     if (threadIdx.x == 0) {
+      const int t_do = p.t_do - (p.gate ? 8 * retries_after(*p.gate) : 0);
       p.exps_out[0] = e;
-      p.exps_out[1] = p.t_do - e;
+      p.exps_out[1] = t_do - e;
+      *p.overflow = 0;  // the MFMA kernels of this attempt raise it
     }
   }
   const int CPR = p.DPc / 8;
@@ -159,6 +190,7 @@ __global__ __launch_bounds__(NTH) void prep_kernel(BwdParams p) {
 // ---- delta = rowsum(dO16 * O16), and dO16 ------------------------------------------
 // One 16-lane group per padded query row; G comes from the prep pass.
 __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
+  if (gated_off(p)) return;
   const int G = p.exps_out[1];
   const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
   const float sdo = ldexp1(ev_of(p, b, h) + G);
@@ -203,6 +235,7 @@ template <int DP, bool CAUSAL, bool HAS_BIAS, int PART, bool DROP>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS || DROP || DP > 128 ? 1 : 2,
                                                                      HAS_BIAS || DROP || DP > 128 ? 1 : 2))) void
 dkdv_kernel(BwdParams p) {
+  if (gated_off(p)) return;
   constexpr bool WANT_DV = PART != 2, WANT_DK = PART != 1;
   constexpr int BQ = 32, BK = 128;
   constexpr int KS = DP / 16, DB = DP / 32, CPR = DP / 8;
@@ -443,7 +476,8 @@ dkdv_kernel(BwdParams p) {
   __syncthreads();
   float* sOut = reinterpret_cast<float*>(smem);  // 64 keys x DP floats
   const float sk_out = ldexp1(-a - G) * p.scale, sv_out = ldexp1(-ev - G);
-  bool bad = false;
+  float mx = 0.f;  // largest |dk16| / |dv16| of this thread
+  bool nonfinite = false;
 #pragma unroll
   for (int pass = 0; pass < 4; ++pass) {
     const int kind = pass >> 1, half = pass & 1;
@@ -461,7 +495,11 @@ dkdv_kernel(BwdParams p) {
           const int kl = (wave & 1) * 32 + 8 * (r >> 2) + 4 * fk + (r & 3);
           const int d = db * 32 + fr;
           const float x = acc[db][r];
-          if (k0 + half * 64 + kl < p.Sk && d < p.D) bad |= bad16(x * chk);
+          if (k0 + half * 64 + kl < p.Sk && d < p.D) {
+            const float ax = fabsf(x * chk);
+            mx = fmaxf(mx, ax);
+            nonfinite |= !(ax <= __FLT_MAX__);
+          }
           sOut[kl * DP + d] = x * so;
         }
     }
@@ -479,7 +517,7 @@ dkdv_kernel(BwdParams p) {
     }
     __syncthreads();
   }
-  if (bad) atomicOr(p.overflow, 1);
+  record_max(p, mx, nonfinite);
 }
 
 // ---- dQ --------------------------------------------------------------------------
@@ -490,6 +528,7 @@ dkdv_kernel(BwdParams p) {
 template <int DP, bool CAUSAL, bool HAS_BIAS, bool DROP>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS || DP > 128 ? 1 : 2, HAS_BIAS || DP > 128 ? 1 : 2))) void
 dq_kernel(BwdParams p) {
+  if (gated_off(p)) return;
   constexpr int BQ = 128, BKV = 32;
   constexpr int KS = DP / 16, DB = DP / 32;
   constexpr int TILE = BKV * DP * 2;  // 32 key rows of K16 (or V16)
@@ -651,7 +690,8 @@ dq_kernel(BwdParams p) {
   }
 
   // dQ^T accumulators: lane col = query (fr), rows d = db*32 + 8*(r/4) + 4*fk + r%4
-  bool bad = false;
+  float mx = 0.f;  // largest |dq16| of this thread
+  bool nonfinite = false;
   if (qrow < p.Sq) {
     const float so = ldexp1(a - G) * p.scale;
     const int64_t orow = ((int64_t)bh * p.Sq + qrow) * p.D;
@@ -665,13 +705,15 @@ dq_kernel(BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float x = dq[db][4 * rq + e];
-          bad |= bad16(x * p.scale);
+          const float ax = fabsf(x * p.scale);
+          mx = fmaxf(mx, ax);
+          nonfinite |= !(ax <= __FLT_MAX__);
           y[e] = x * so;
         }
         *reinterpret_cast<uint2*>(p.dq + orow + d) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
       }
   }
-  if (bad) atomicOr(p.overflow, 1);
+  record_max(p, mx, nonfinite);
 }
 
 struct BwdWs {
@@ -740,7 +782,7 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
                               const int64_t* v_strides, const int64_t* do_strides, const void* bias,
                               const int64_t* bias_strides, float scale, int causal, int t_do, float dropout_p,
                               uint64_t seed, void* dq, void* dk, void* dv, int32_t* exps_out, int32_t* overflow,
-                              void* ws, int64_t ws_bytes, void* stream) {
+                              const int32_t* gate, void* ws, int64_t ws_bytes, void* stream) {
   TB_CHECK(B >= 0 && H > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0 && H % Hkv == 0, "attn_bwd: bad shape");
   TB_CHECK(D > 0 && D % 8 == 0 && D <= 256, "attn_bwd: head dim must be a multiple of 8 up to 256");
   TB_CHECK(dropout_p >= 0.f && dropout_p < 1.f, "attn_bwd: dropout_p must be in [0, 1)");
@@ -758,9 +800,12 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
   if (B == 0 || Sq == 0 || Sk == 0) return 0;
   hipStream_t st = as_stream(stream);
   float* part = reinterpret_cast<float*>(ws);
-  if (int rc = launch_head_amax_partial(dout, TBF16_DT_BF16, B, H, Sq, D, do_strides[0], do_strides[1], do_strides[2],
-                                        part, w.nch, st))
-    return rc;
+  // a gated attempt reuses the dO maxima its gate's attempt left in the workspace
+  if (!gate) {
+    if (int rc = launch_head_amax_partial(dout, TBF16_DT_BF16, B, H, Sq, D, do_strides[0], do_strides[1],
+                                          do_strides[2], part, w.nch, st))
+      return rc;
+  }
   BwdParams p;
   p.q = (const uint16_t*)q; p.k = (const uint16_t*)k; p.v = (const uint16_t*)v;
   p.o16 = (const uint16_t*)o16; p.dout = (const uint16_t*)dout; p.lse = lse; p.exps_fwd = exps_fwd;
@@ -775,7 +820,7 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
   set_dropout(dropout_p, seed, p.drop_lo, p.drop_hi, p.drop_thr, p.drop_scale);
   p.part_do = part; p.nch_do = (int)w.nch;
   p.delta = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + w.off_delta);
-  p.exps_out = exps_out; p.overflow = overflow;
+  p.exps_out = exps_out; p.overflow = overflow; p.gate = gate;
   p.dq = (uint16_t*)dq; p.dk = (uint16_t*)dk; p.dv = (uint16_t*)dv;
   char* wsb = reinterpret_cast<char*>(ws);
   p.q16 = reinterpret_cast<uint16_t*>(wsb + w.off_q16);
@@ -784,8 +829,12 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
   p.v16 = reinterpret_cast<uint16_t*>(wsb + w.off_v16);
   p.Sqp = (int)w.Sqp; p.Skp = (int)w.Skp; p.DPc = (int)w.DP;
   {
+    // q16, k16 and v16 do not depend on t_do: a gated attempt finds them in the
+    // workspace and only needs block (0, 0), which derives e and G (its rows are
+    // rewritten with the same values)
     const int64_t rpb = NTH / (w.DP / 8);
-    prep_kernel<<<dim3((unsigned)cdiv(std::max(w.Sqp, w.Skp), 4 * rpb), (unsigned)(B * H + 2 * B * Hkv)), NTH, 0, st>>>(p);
+    const dim3 grid = gate ? dim3(1, 1) : dim3((unsigned)cdiv(std::max(w.Sqp, w.Skp), 4 * rpb), (unsigned)(B * H + 2 * B * Hkv));
+    prep_kernel<<<grid, NTH, 0, st>>>(p);
     TB_LAUNCH_CHECK("attn_bwd/prep");
   }
   delta_kernel<<<dim3((unsigned)cdiv(w.Sqp, 16), (unsigned)(B * H)), NTH, 0, st>>>(p);

@@ -14,7 +14,7 @@ import pathlib
 import torch
 
 _LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libtbf16_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DT_BF16, DT_F16 = 0, 1
 
@@ -54,7 +54,7 @@ _SIGS = {
                            P, I64, P]),
     "tbf16_attn_bwd_ws_bytes": (SZ, [I64, I64, I64, I64, I64, I64]),
     "tbf16_attn_bwd": (I, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, PI64, PI64, PI64, PI64, P, PI64, F,
-                           I, I, F, U64, P, P, P, P, P, P, I64, P]),
+                           I, I, F, U64, P, P, P, P, P, P, P, I64, P]),
 }
 
 
