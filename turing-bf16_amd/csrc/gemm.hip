@@ -434,40 +434,55 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   }
 
   // ---- epilogue: (acc * sa[m]) * sb[n] + bias[n] -> bf16 straight from registers ----
-  // Lane l holds columns 8 q + 4 (l / 32) .. + 3 of row l % 32 for q = 0..3; one
-  // v_permlane32_swap per dword pairs q = 2p (kept by lanes < 32) with q = 2p + 1
-  // (kept by lanes >= 32), so every lane stores 8 consecutive columns (16 bytes)
-  // and no LDS round trip or barrier is needed.
+  // Lane l holds columns 8 q + 4 (l / 32) .. + 3 of row l % 32 for q = 0..3. Two
+  // exchanges regroup them without LDS or a barrier: v_permlane32_swap pairs q = 2p
+  // (kept by lanes < 32) with q = 2p + 1 (kept by lanes >= 32), so a lane holds 8
+  // columns (16 bytes) of its row; v_permlane16_swap then pairs p = 0 with p = 1
+  // between 16-lane rows, so each store instruction writes 64 contiguous bytes of
+  // each of 16 rows (lane l: row l % 16 (+ 16 for the second store), columns 0 /
+  // 16 / 8 / 24 of the 32-column block for l / 16 = 0 / 1 / 2 / 3).
+  const int rl = lane & 15, cq = lane >> 4;
+  const int cl = ((cq & 1) << 4) | ((cq >> 1) << 3);
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
-    const int ml = wm * TM + j * 32 + fr;  // row within the tile
+    const int ml = wm * TM + j * 32 + fr;  // this lane's row before the exchanges
     const float sa = sa_l[ml];
-    const bool mok = m0 + ml < M;
+    const int r0 = m0 + wm * TM + j * 32 + rl;  // rows stored by this lane
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
+      uint32_t w[4][2];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = wn * TN + i * 32 + 8 * q + 4 * fk;
+        const float4 sb = *reinterpret_cast<const float4*>(sb_l + nl);
+        const uint2 bw = *reinterpret_cast<const uint2*>(bias_l + nl);
+        const float y0 = fmaf(acc[i][j][4 * q + 0] * sa, sb.x, bf16_lo(bw.x));
+        const float y1 = fmaf(acc[i][j][4 * q + 1] * sa, sb.y, bf16_hi(bw.x));
+        const float y2 = fmaf(acc[i][j][4 * q + 2] * sa, sb.z, bf16_lo(bw.y));
+        const float y3 = fmaf(acc[i][j][4 * q + 3] * sa, sb.w, bf16_hi(bw.y));
+        w[q][0] = pack_bf16(y0, y1);
+        w[q][1] = pack_bf16(y2, y3);
+      }
+      // v[p]: 16 bytes of row l % 32, columns 16 p + 8 (l / 32) .. + 7
+      uint32_t v[2][4];
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        uint32_t w[2][2];
+        const auto d0 = __builtin_amdgcn_permlane32_swap(w[2 * p][0], w[2 * p + 1][0], false, false);
+        const auto d1 = __builtin_amdgcn_permlane32_swap(w[2 * p][1], w[2 * p + 1][1], false, false);
+        v[p][0] = d0[0]; v[p][1] = d1[0]; v[p][2] = d0[1]; v[p][3] = d1[1];
+      }
+      // x: rows 0..15 of the 32-row block, y: rows 16..31
+      uint32_t x[4], y[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int q = 2 * p + h;
-          const int nl = wn * TN + i * 32 + 8 * q + 4 * fk;
-          const float4 sb = *reinterpret_cast<const float4*>(sb_l + nl);
-          const uint2 bw = *reinterpret_cast<const uint2*>(bias_l + nl);
-          const float y0 = fmaf(acc[i][j][4 * q + 0] * sa, sb.x, bf16_lo(bw.x));
-          const float y1 = fmaf(acc[i][j][4 * q + 1] * sa, sb.y, bf16_hi(bw.x));
-          const float y2 = fmaf(acc[i][j][4 * q + 2] * sa, sb.z, bf16_lo(bw.y));
-          const float y3 = fmaf(acc[i][j][4 * q + 3] * sa, sb.w, bf16_hi(bw.y));
-          w[h][0] = pack_bf16(y0, y1);
-          w[h][1] = pack_bf16(y2, y3);
-        }
-        // [0]: lanes < 32 keep their own q = 2p dword, lanes >= 32 receive lane
-        // l - 32's q = 2p + 1 dword; [1]: lanes < 32 receive lane l + 32's q = 2p
-        // dword, lanes >= 32 keep their own q = 2p + 1 dword
-        const auto d0 = __builtin_amdgcn_permlane32_swap(w[0][0], w[1][0], false, false);
-        const auto d1 = __builtin_amdgcn_permlane32_swap(w[0][1], w[1][1], false, false);
-        const int n = n0 + wn * TN + i * 32 + 16 * p + 8 * fk;
-        if (mok && n < N) stg16(C + (int64_t)(m0 + ml) * ldc + n, make_uint4(d0[0], d1[0], d0[1], d1[1]));
+      for (int d = 0; d < 4; ++d) {
+        const auto e = __builtin_amdgcn_permlane16_swap(v[0][d], v[1][d], false, false);
+        x[d] = e[0];
+        y[d] = e[1];
+      }
+      const int n = n0 + wn * TN + i * 32 + cl;
+      if (n < N) {
+        if (r0 < M) stg16(C + (int64_t)r0 * ldc + n, make_uint4(x[0], x[1], x[2], x[3]));
+        if (r0 + 16 < M) stg16(C + (int64_t)(r0 + 16) * ldc + n, make_uint4(y[0], y[1], y[2], y[3]));
       }
     }
   }
