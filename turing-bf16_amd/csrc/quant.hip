@@ -31,6 +31,8 @@ __global__ __launch_bounds__(256) void row_exps_kernel(const uint16_t* __restric
 }
 
 // quantize_rows: amax pass, then y = fp16(x * 2^p) (small_kernels.cu:35-74).
+// Rows of up to kRegChunks x 512 elements are read once, into registers.
+constexpr int kRegChunks = 16;
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t R, int K,
                                                             int64_t ldx, int t, int l1, uint16_t* __restrict__ y,
                                                             int64_t ldy, float* __restrict__ s_inv,
@@ -39,12 +41,46 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const uint16_t* __re
   const int lane = threadIdx.x & 63;
   if (row >= R) return;
   const uint16_t* xr = x + row * ldx;
-  const float amax = row_amax_wave(xr, K, lane, l1 != 0);
-  const int p = pow2_exp(amax, t);
-  const float s = pow2f(p);
   const uint4* src = reinterpret_cast<const uint4*>(xr);
   uint4* dst = reinterpret_cast<uint4*>(y + row * ldy);
-  for (int i = lane; i < (K >> 3); i += kWave) dst[i] = cvt_bf16x8_f16x8(src[i], s);
+  const int K8 = K >> 3;
+  int p;
+  if (K8 <= kWave * kRegChunks) {
+    // the row stays in registers between its reduction and its conversion (one
+    // read of x); same element order and arithmetic as row_amax_wave
+    uint4 v[kRegChunks];
+#pragma unroll
+    for (int c = 0; c < kRegChunks; ++c) v[c] = lane + c * kWave < K8 ? src[lane + c * kWave] : make_uint4(0, 0, 0, 0);
+    float amax;
+    if (l1) {
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < kRegChunks; ++c)
+        if (lane + c * kWave < K8)
+          acc += (double)fabsf(bf16_lo(v[c].x)) + (double)fabsf(bf16_hi(v[c].x)) + (double)fabsf(bf16_lo(v[c].y)) +
+                 (double)fabsf(bf16_hi(v[c].y)) + (double)fabsf(bf16_lo(v[c].z)) + (double)fabsf(bf16_hi(v[c].z)) +
+                 (double)fabsf(bf16_lo(v[c].w)) + (double)fabsf(bf16_hi(v[c].w));
+      amax = (float)wave_sum_d(acc);
+    } else {
+      float m = 0.f;  // zero chunks past the row end leave the maximum alone
+#pragma unroll
+      for (int c = 0; c < kRegChunks; ++c)
+        m = fmaxf(m, fmaxf(fmaxf(fmaxf(fabsf(bf16_lo(v[c].x)), fabsf(bf16_hi(v[c].x))),
+                                 fmaxf(fabsf(bf16_lo(v[c].y)), fabsf(bf16_hi(v[c].y)))),
+                           fmaxf(fmaxf(fabsf(bf16_lo(v[c].z)), fabsf(bf16_hi(v[c].z))),
+                                 fmaxf(fabsf(bf16_lo(v[c].w)), fabsf(bf16_hi(v[c].w))))));
+      amax = wave_max(m);
+    }
+    p = pow2_exp(amax, t);
+    const float s = pow2f(p);
+#pragma unroll
+    for (int c = 0; c < kRegChunks; ++c)
+      if (lane + c * kWave < K8) dst[lane + c * kWave] = cvt_bf16x8_f16x8(v[c], s);
+  } else {
+    p = pow2_exp(row_amax_wave(xr, K, lane, l1 != 0), t);
+    const float s = pow2f(p);
+    for (int i = lane; i < K8; i += kWave) dst[i] = cvt_bf16x8_f16x8(src[i], s);
+  }
   if (lane == 0) {
     s_inv[row] = ldexp1(-p);
     if (exps) exps[row] = p;
