@@ -16,8 +16,9 @@
 // (tbf16/autograd.py:184-187). A launch given a `gate` (the word of an earlier
 // attempt at the same t_do) runs only if that attempt overflowed, at t_do - 8 r with
 // r the retries the reference would take: all values scale by exactly 2^-8 per
-// retry, so r follows from the earlier maximum. Every kernel of a gated launch
-// returns at once when r = 0, so the retry needs no host round trip.
+// retry, so r follows from the earlier maximum. A gated launch skips prep (q16,
+// k16, v16 and e are already in the workspace and exps_out) and its other kernels
+// return at once when r = 0, so the retry needs no host round trip.
 //
 // Kernels (4 waves, v_mfma_f32_32x32x16_f16):
 //   prep:    q16, k16, v16 (one launch, memory-bound); its first block derives e, G.
@@ -145,14 +146,12 @@ __device__ __forceinline__ void record_max(const BwdParams& p, float mx, bool no
 // q heads first, then the k and v heads. Zeros past the real rows and columns.
 // Block (0, 0) also derives e and G (they are needed by the delta pass only).
 __global__ __launch_bounds__(NTH) void prep_kernel(BwdParams p) {
-  if (gated_off(p)) return;
   __shared__ int red[4];
   if (blockIdx.x == 0 && blockIdx.y == 0) {
     const int e = compute_e(p, red);
     if (threadIdx.x == 0) {
-      const int t_do = p.t_do - (p.gate ? 8 * retries_after(*p.gate) : 0);
       p.exps_out[0] = e;
-      p.exps_out[1] = t_do - e;
+      p.exps_out[1] = p.t_do - e;
       *p.overflow = 0;  // the MFMA kernels of this attempt raise it
     }
   }
@@ -191,7 +190,18 @@ __global__ __launch_bounds__(NTH) void prep_kernel(BwdParams p) {
 // One 16-lane group per padded query row; G comes from the prep pass.
 __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
   if (gated_off(p)) return;
-  const int G = p.exps_out[1];
+  // a gated retry (no prep launch): G at the retried t_do from the first attempt's
+  // e; block (0, 0) publishes it for the MFMA kernels and clears the overflow word
+  int G;
+  if (p.gate) {
+    G = p.t_do - 8 * retries_after(*p.gate) - p.exps_out[0];
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+      p.exps_out[1] = G;
+      *p.overflow = 0;
+    }
+  } else {
+    G = p.exps_out[1];
+  }
   const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
   const float sdo = ldexp1(ev_of(p, b, h) + G);
   const int row = blockIdx.x * 16 + (threadIdx.x >> 4), l16 = threadIdx.x & 15;
@@ -828,13 +838,11 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
   p.k16 = reinterpret_cast<uint16_t*>(wsb + w.off_k16);
   p.v16 = reinterpret_cast<uint16_t*>(wsb + w.off_v16);
   p.Sqp = (int)w.Sqp; p.Skp = (int)w.Skp; p.DPc = (int)w.DP;
-  {
-    // q16, k16 and v16 do not depend on t_do: a gated attempt finds them in the
-    // workspace and only needs block (0, 0), which derives e and G (its rows are
-    // rewritten with the same values)
+  // q16, k16, v16 and e do not depend on t_do: a gated attempt finds them in the
+  // workspace and exps_out, and its delta pass derives G
+  if (!gate) {
     const int64_t rpb = NTH / (w.DP / 8);
-    const dim3 grid = gate ? dim3(1, 1) : dim3((unsigned)cdiv(std::max(w.Sqp, w.Skp), 4 * rpb), (unsigned)(B * H + 2 * B * Hkv));
-    prep_kernel<<<grid, NTH, 0, st>>>(p);
+    prep_kernel<<<dim3((unsigned)cdiv(std::max(w.Sqp, w.Skp), 4 * rpb), (unsigned)(B * H + 2 * B * Hkv)), NTH, 0, st>>>(p);
     TB_LAUNCH_CHECK("attn_bwd/prep");
   }
   delta_kernel<<<dim3((unsigned)cdiv(w.Sqp, 16), (unsigned)(B * H)), NTH, 0, st>>>(p);
