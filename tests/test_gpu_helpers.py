@@ -329,3 +329,30 @@ def test_attn_backward_device_retry_reports_persistent_overflow(dev):
     ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="device")
     with pytest.raises(FloatingPointError):
         ag.check_pending(block=True)
+
+
+def test_attn_backward_device_retry_in_a_graph(dev):
+    """The device-mode backward (both the first attempt and the gated retry) captured
+    in a HIP graph: three replays, with eager work between them, each equal bit for
+    bit to the eager result, in the case that retries once."""
+    q, k, v, do = _dominant_key_case(dev, 4096)
+    sc = 1 / 8
+    o, lse, o16, exps = attention.attn_forward(q, k, v, None, False, sc, 0, True, True)
+    want = ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="device")
+    ag.check_pending(block=True)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up off the default stream, as capture wants
+        ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="device")
+    torch.cuda.current_stream().wait_stream(side)
+    ag.check_pending(block=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        got = ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="device")
+    for _ in range(3):
+        torch.randn(1 << 20, device=dev).sum()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        for n, a, b in zip(("dq", "dk", "dv", "exps"), want, got):
+            assert torch.equal(a, b), n
