@@ -20,7 +20,8 @@ convolutions (the conv.py path; not a BASELINE config) and torch's own fp16
 kernels on the same shapes. `roofline` prices the dominant kernel (the GEMM)
 against the dense fp16 MFMA peak from its own event-timed launches;
 `cpu_baseline` times the oracle's restatement of the headline workload on the
-host cores.
+host cores; configs[0], the decode sweep and the 4k attention carry CPU legs of
+their own (the oracle's restatements of the reference's arithmetic).
 """
 from __future__ import annotations
 
@@ -391,6 +392,50 @@ def cpu_cfg1():
                       f"{_cpu_model()}"}
 
 
+def cpu_small_m():
+    """CPU leg of the decode sweep: the oracle's restatement of the
+    reference's own regime on the host cores (M = 1: fp32 GEMV; M >= 2: L1 row
+    scales and an fp16 C, ops.py:163-178), median of 3 calls per M, in the GPU
+    line's bytes per call."""
+    import torch
+    import workloads as W
+    from oracle import tbf16_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    w, xs = W.cfg3_small_m()
+    N, K = w.shape
+    w16o, wso = O.prepare_weight(w)
+    per_m = {}
+    for M, x in xs.items():
+        fn = (lambda: O.gemv(x, w16o, wso)) if M == 1 else (lambda: O.linear_cublas_path(x, w16o, wso))
+        fn()
+        sec, n = _cpu_repeat(fn, 3, 0.0)
+        byt = 2 * N * K + 2 * M * K + 2 * M * N + 4 * N + 4 * M
+        per_m[str(M)] = {"us": round(sec * 1e6, 1), "GBs": round(byt / sec / 1e9, 2)}
+    return {"unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port", "per_M": per_m,
+            "sample": f"one full call per M (oracle.gemv / oracle.linear_cublas_path), median of 3, {_cpu_model()}"}
+
+
+def cpu_attention():
+    """CPU leg of configs[3] at S = 4096: the oracle's restatement of the reference's
+    inference arithmetic (prepare_qkv's fp16 copies, fp32 logits and softmax, fp16
+    P and O, head_scale; attention.py:56-65) on the host cores, median of 3 calls,
+    in causal TFLOPS."""
+    import torch
+    import workloads as W
+    from oracle import tbf16_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    q, k, v = W.cfg4_attention(4096)
+    B, H, S, D = q.shape
+    fn = lambda: O.sdpa_reference_arith(q, k, v, causal=True)  # noqa: E731
+    sec, n = _cpu_repeat(fn, 3, 0.0)
+    fl = 2.0 * B * H * S * S * D
+    return {"S": S, "value": round(fl / sec / 1e12, 4), "unit": "TFLOPS", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"full configs[3] call at S = 4096 (oracle.sdpa_reference_arith, the full "
+                                      f"S x S logits masked), median of {n}, {sec:.2f} s each, {_cpu_model()}"}
+
+
 def profile_run(what: str):
     """A few launches of one workload, for rocprofv3 counter passes."""
     import torch
@@ -519,6 +564,8 @@ def main():
     line.update(extras)
     if not a.no_cpu and not a.quick:
         line["configs0_linear"]["cpu_baseline"] = cpu_cfg1()
+        line["small_m_decode"]["cpu_baseline"] = cpu_small_m()
+        line["attention_fwd_cpu_baseline"] = cpu_attention()
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
