@@ -434,13 +434,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   }
 
   // ---- epilogue: (acc * sa[m]) * sb[n] + bias[n] -> bf16 straight from registers ----
-  // Lane l holds columns 8 q + 4 (l / 32) .. + 3 of row l % 32 for q = 0..3. Two
-  // exchanges regroup them without LDS or a barrier: v_permlane32_swap pairs q = 2p
+  // Lane l holds columns 8 q + 4 (l / 32) .. + 3 of row l % 32 for q = 0..3.
+  // Exchanges regroup them without LDS or a barrier: v_permlane32_swap pairs q = 2p
   // (kept by lanes < 32) with q = 2p + 1 (kept by lanes >= 32), so a lane holds 8
   // columns (16 bytes) of its row; v_permlane16_swap then pairs p = 0 with p = 1
-  // between 16-lane rows, so each store instruction writes 64 contiguous bytes of
-  // each of 16 rows (lane l: row l % 16 (+ 16 for the second store), columns 0 /
-  // 16 / 8 / 24 of the 32-column block for l / 16 = 0 / 1 / 2 / 3).
+  // between 16-lane rows (lane l: row l % 16, or + 16, columns 0 / 16 / 8 / 24 of
+  // the 32-column block for l / 16 = 0 / 1 / 2 / 3); where FN is even, a DPP
+  // row_ror:8 exchange between lanes l and l ^ 8 then pairs blocks i - 1 and i, so
+  // each store instruction writes whole 128-byte rows (8 rows x 64 columns) and L2
+  // writes back exactly y (WRITE_SIZE = y; 64-byte runs had read 1.38 x).
   const int rl = lane & 15, cq = lane >> 4;
   const int cl = ((cq & 1) << 4) | ((cq >> 1) << 3);
 #pragma unroll
@@ -448,6 +450,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
     const int ml = wm * TM + j * 32 + fr;  // this lane's row before the exchanges
     const float sa = sa_l[ml];
     const int r0 = m0 + wm * TM + j * 32 + rl;  // rows stored by this lane
+    uint32_t xa[4], ya[4];  // block i - 1's x / y, held for the third exchange
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
       uint32_t w[4][2];
@@ -479,10 +482,41 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
         x[d] = e[0];
         y[d] = e[1];
       }
-      const int n = n0 + wn * TN + i * 32 + cl;
-      if (n < N) {
-        if (r0 < M) stg16(C + (int64_t)r0 * ldc + n, make_uint4(x[0], x[1], x[2], x[3]));
-        if (r0 + 16 < M) stg16(C + (int64_t)(r0 + 16) * ldc + n, make_uint4(y[0], y[1], y[2], y[3]));
+      if constexpr (FN % 2 == 0) {
+        if (i % 2 == 0) {
+#pragma unroll
+          for (int d = 0; d < 4; ++d) { xa[d] = x[d]; ya[d] = y[d]; }
+          continue;
+        }
+        // third exchange: lane l and lane l ^ 8 (DPP row_ror:8) trade so that one
+        // store writes rows 0..7 (or 8..15) with blocks i - 1 and i side by side
+        const bool hi8 = (lane & 8) != 0;
+        uint32_t f[4], s2[4], g[4], s3[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t tx = __builtin_amdgcn_mov_dpp((int)xa[d], 0x128, 0xF, 0xF, false);
+          const uint32_t tb = __builtin_amdgcn_mov_dpp((int)x[d], 0x128, 0xF, 0xF, false);
+          f[d] = hi8 ? tb : xa[d];
+          s2[d] = hi8 ? x[d] : tx;
+          const uint32_t uy = __builtin_amdgcn_mov_dpp((int)ya[d], 0x128, 0xF, 0xF, false);
+          const uint32_t ub = __builtin_amdgcn_mov_dpp((int)y[d], 0x128, 0xF, 0xF, false);
+          g[d] = hi8 ? ub : ya[d];
+          s3[d] = hi8 ? y[d] : uy;
+        }
+        const int rb = m0 + wm * TM + j * 32 + (lane & 7);
+        const int n = n0 + wn * TN + (i - 1 + (hi8 ? 1 : 0)) * 32 + cl;
+        if (n < N) {
+          if (rb < M) stg16(C + (int64_t)rb * ldc + n, make_uint4(f[0], f[1], f[2], f[3]));
+          if (rb + 8 < M) stg16(C + (int64_t)(rb + 8) * ldc + n, make_uint4(s2[0], s2[1], s2[2], s2[3]));
+          if (rb + 16 < M) stg16(C + (int64_t)(rb + 16) * ldc + n, make_uint4(g[0], g[1], g[2], g[3]));
+          if (rb + 24 < M) stg16(C + (int64_t)(rb + 24) * ldc + n, make_uint4(s3[0], s3[1], s3[2], s3[3]));
+        }
+      } else {
+        const int n = n0 + wn * TN + i * 32 + cl;
+        if (n < N) {
+          if (r0 < M) stg16(C + (int64_t)r0 * ldc + n, make_uint4(x[0], x[1], x[2], x[3]));
+          if (r0 + 16 < M) stg16(C + (int64_t)(r0 + 16) * ldc + n, make_uint4(y[0], y[1], y[2], y[3]));
+        }
       }
     }
   }
