@@ -74,9 +74,11 @@ int tbf16_quantize_cols_t(const void* x, int64_t R, int64_t K, int64_t ldx, int 
  * l1) computed inside this call. One bf16 rounding.
  * x bf16 (M, K); w16 fp16 (N, K); ws fp32 (N,); bias bf16 (N,) or NULL; y bf16
  * (M, N). cfg < 0 picks the tile shape. workspace: tbf16_linear_ws_bytes(M, K, N,
- * cfg) bytes, 16-byte aligned; its first M int32 receive the row exponents p (the
- * decode configurations also keep x's scaled fp16 copy there, as the reference's
- * small-M path does). Replaces linear (tbf16/csrc/gemm_sm75.cu:257-284) and, at
+ * cfg) bytes, 16-byte aligned; its first M int32 receive the row exponents p.
+ * With the decode configurations, and with tiles of at most 128 columns at K >=
+ * 1024, x is quantised once, as the reference's small-M path does: the row
+ * inverse scales and x's scaled fp16 copy go into the workspace too, and the
+ * GEMM runs on fp16 operands (the same output as converting x inside it). Replaces linear (tbf16/csrc/gemm_sm75.cu:257-284) and, at
  * 2 <= M < 256, quantize_rows + cuBLAS + epilogue (tbf16/ops.py:163-178) without
  * its fp16 intermediate. */
 size_t tbf16_linear_ws_bytes(int64_t M, int64_t K, int64_t N, int cfg);
@@ -88,9 +90,10 @@ int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w
  * workspace lives in a static device array of TBF16_NOALLOC_SCRATCH_BYTES per GPU
  * (12 MiB, held until the process ends). No counterpart in the reference: it is
  * for callers that cannot allocate (code under HIP graph capture, serving loops,
- * harnesses that forbid hipMalloc). M above TBF16_NOALLOC_MAX_ROWS, or a call whose
- * tbf16_linear_ws_bytes exceeds the array (decode-sized M with K beyond ~24k), is
- * rejected (TBF16_EINVAL). Calls that overlap on one GPU (concurrent streams or
+ * harnesses that forbid hipMalloc). Where x's fp16 copy does not fit in the array,
+ * a tile configuration converts x inside the GEMM instead (the same output); M
+ * above TBF16_NOALLOC_MAX_ROWS, or a decode-sized call (M <= 128) whose copy does
+ * not fit (K beyond ~24k), is rejected (TBF16_EINVAL). Calls that overlap on one GPU (concurrent streams or
  * threads) share the array and race. Same arguments and results as tbf16_linear
  * otherwise. */
 #define TBF16_NOALLOC_MAX_ROWS (1 << 20)

@@ -1081,15 +1081,30 @@ int launch_quantize_rows(const void* x, int64_t R, int64_t K, int64_t ldx, int t
 
 namespace {
 
-// Workspace of tbf16_linear: the row exponents (int32 (M,)) and, where the chosen
-// configuration takes fp16 a (the decode kernel), the row inverse scales (fp32
-// (M,)) and the scaled fp16 copy of x (M, K), each 256-byte aligned.
+// Whether tbf16_linear quantises x once (row exponents, inverse scales and the
+// fp16 rows into its workspace) and runs the GEMM on fp16 operands, instead of
+// converting x inside the GEMM. The decode kernel takes fp16 a only. Tiles of at
+// most 128 columns convert each x tile once per column block (64 times at N =
+// 4096 with 64-column tiles), which the one pass saves: bit-identical output,
+// 256x4096x4096 34.6 -> 27.7 us, 1024x4096x4096 56.9 -> 50.3, 2048x4096x4096 84.4
+// -> 77.1 (128-column tiles). 256-column tiles convert x 16 times at N = 4096
+// and gain nothing there (4096^3: the extra pass costs more than it saves), and
+// at K < 1024 the pass costs about what it saves (200x2560x768: 10.0 vs 10.6 us).
+bool quantize_once(int cfg, int64_t K) {
+  if (cfg < 0 || cfg >= kNumCfgs) return false;
+  const TileCfg& c = kCfgs[cfg];
+  return c.stream || (!c.skinny && c.bn <= 128 && K >= 1024);
+}
+
+// Workspace of tbf16_linear: the row exponents (int32 (M,)) and, where x is
+// quantised once (`quantize_once`), the row inverse scales (fp32 (M,)) and the
+// scaled fp16 copy of x (M, K), each 256-byte aligned.
 struct LinearWs {
   size_t exps, sinv, x16, bytes;
 };
 LinearWs linear_ws(int64_t M, int64_t K, int cfg) {
   LinearWs w{0, 0, 0, align_up((size_t)M * 4, 256)};
-  if (cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg].stream) {
+  if (quantize_once(cfg, K)) {
     w.sinv = w.bytes;
     w.x16 = w.sinv + align_up((size_t)M * 4, 256);
     w.bytes = w.x16 + (size_t)M * (size_t)K * 2;
@@ -1097,17 +1112,19 @@ LinearWs linear_ws(int64_t M, int64_t K, int cfg) {
   return w;
 }
 
+// fused: convert x inside the GEMM even where `quantize_once` holds (same output;
+// for a workspace too small for the fp16 copy of x). The decode kernel cannot.
 int linear_into(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N, int64_t ldw,
                 const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg, uint8_t* wsp,
-                hipStream_t st) {
+                bool fused, hipStream_t st) {
   const LinearWs w = linear_ws(M, K, cfg);
   int32_t* exps = reinterpret_cast<int32_t*>(wsp + w.exps);
-  if (!kCfgs[cfg].stream) {
+  if (!quantize_once(cfg, K) || (fused && !kCfgs[cfg].stream)) {
     if (int rc = launch_row_exps(x, M, K, ldx, t, l1, exps, nullptr, st)) return rc;
     return launch_gemm<true>(cfg, x, ldx, exps, nullptr, w16, ldw, ws, bias, y, ldy, M, N, K, st);
   }
-  // decode: x quantised once (exponents, inverse scales, fp16 rows), then the GEMM
-  // on fp16 operands; the same fp16 values the fused kernels convert in registers
+  // x quantised once (exponents, inverse scales, fp16 rows), then the GEMM on fp16
+  // operands: the same fp16 values the fused kernels convert in registers
   float* sinv = reinterpret_cast<float*>(wsp + w.sinv);
   void* x16 = wsp + w.x16;
   if (int rc = launch_quantize_rows(x, M, K, ldx, t, l1, x16, K, sinv, exps, st)) return rc;
@@ -1129,7 +1146,7 @@ extern "C" int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, co
   TB_CHECK(cfg < kNumCfgs, "bad cfg");
   if (M == 0 || N == 0) return 0;
   return linear_into(x, M, K, ldx, w16, N, ldw, ws, bias, y, ldy, t, l1, cfg < 0 ? pick_cfg(M, N, true) : cfg,
-                     static_cast<uint8_t*>(workspace), as_stream(stream));
+                     static_cast<uint8_t*>(workspace), false, as_stream(stream));
 }
 
 // ---- tbf16_linear_noalloc: the workspace in a static device array ---------------
@@ -1171,13 +1188,16 @@ extern "C" int tbf16_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t
   TB_CHECK(cfg < kNumCfgs, "bad cfg");
   if (M == 0 || N == 0) return 0;
   const int c = cfg < 0 ? pick_cfg(M, N, true) : cfg;
-  const size_t need = linear_ws(M, K, c).bytes;
+  // where the fp16 copy of x does not fit, a tile configuration converts x inside
+  // the GEMM instead (the same output); the decode kernel needs the copy
+  const bool fused = !kCfgs[c].stream && linear_ws(M, K, c).bytes > TBF16_NOALLOC_SCRATCH_BYTES;
+  const size_t need = fused ? linear_ws(M, K, -1).bytes : linear_ws(M, K, c).bytes;
   TB_CHECK(need <= TBF16_NOALLOC_SCRATCH_BYTES,
            "linear_noalloc: %lld x %lld needs %zu workspace bytes, beyond the scratch limit of %d bytes", (long long)M,
            (long long)K, need, TBF16_NOALLOC_SCRATCH_BYTES);
   uint8_t* wsp = nullptr;
   if (int rc = scratch_ptr(&wsp)) return rc;
-  return linear_into(x, M, K, ldx, w16, N, ldw, ws, bias, y, ldy, t, l1, c, wsp, as_stream(stream));
+  return linear_into(x, M, K, ldx, w16, N, ldw, ws, bias, y, ldy, t, l1, c, wsp, fused, as_stream(stream));
 }
 
 extern "C" int tbf16_linear_exps(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t* exps,
