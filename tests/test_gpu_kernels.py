@@ -149,6 +149,28 @@ def test_gemm_small_integers_bit_exact(dev, cfg, K):
     assert np.array_equal(e.cpu().numpy(), O.row_exps(a.bfloat16(), 15))
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 4096, 4096), (200, 768, 2560), (300, 264, 3040)])
+def test_linear_split_k(dev, M, N, K):
+    """K split over two blocks per tile (what tbf16_linear picks where the tiles leave
+    half of the CUs idle: configs[0]'s shape, a ragged M and N, a K tail in the second
+    half). Integer-valued products are exact in any summation order, so with an
+    integer bias the output equals the integer product rounded once, bit for bit;
+    on random rows the output stays within the fp64 bound."""
+    assert int(_ext.lib().tbf16_linear_ws_bytes(M, K, N, -1)) >= 2 * M * N * 4  # the split's partial sums
+    g = torch.Generator().manual_seed(7)
+    a = torch.randint(-1, 2, (M, K), generator=g)
+    b = torch.randint(-1, 2, (N, K), generator=g)
+    bias = torch.randint(-8, 9, (N,), generator=g)
+    w16, wsv = ops.prepare_weight(b.bfloat16().to(dev))
+    y = ops.scaled_linear(a.bfloat16().to(dev), w16, wsv, bias.bfloat16().to(dev))
+    assert torch.equal(y.cpu(), ((a @ b.t()).double() + bias.double()).bfloat16())
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    w16, wsv = ops.prepare_weight(w.to(dev))
+    y = ops.scaled_linear(x.to(dev), w16, wsv)
+    assert rel(y.cpu(), x.double() @ w.double().t()) <= TOL
+
+
 def test_gemv_small_integers_bit_exact(dev):
     g = torch.Generator().manual_seed(4)
     K, N = 2560, 1000

@@ -63,7 +63,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
                                                            const uint16_t* __restrict__ B, int64_t ldb,
                                                            const float* __restrict__ b_sinv,
                                                            const uint16_t* __restrict__ bias,
-                                                           uint16_t* __restrict__ C, int64_t ldc, int M, int N, int K) {
+                                                           uint16_t* __restrict__ C, int64_t ldc, int M, int N,
+                                                           int K_all, float* __restrict__ part, int kt_per) {
   constexpr int NT = WM * WN * 64;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / 32, FN = TN / 32;
@@ -97,6 +98,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   const int within = bid % (GM * tiles_n);
   const int m0 = (first + within % gsize) * BM;
   const int n0 = (within / gsize) * BN;
+  // split K (part != nullptr): block (x, y) sums k tiles [y kt_per, (y + 1) kt_per)
+  // of its tile into fp32 partial sums part[y]; the reduction applies the epilogue
+  const int ks = part ? (int)blockIdx.y : 0;
+  const int kbase = ks * kt_per * BK;
+  const int K = part ? min(K_all - kbase, kt_per * BK) : K_all;
 
   // the epilogue's factors (rows past M / columns past N get 0 and are not stored)
   for (int t = tid; t < BM; t += NT) {
@@ -122,8 +128,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   // KEVEN is false (a select on a loaded value makes the compiler wait for that
   // load on the spot, which serialises the register pipeline).
   const int lrow = tid / CPR, lch = tid % CPR;
-  const BufRes arsrc = make_res(A + (int64_t)m0 * lda, min<int64_t>((int64_t)(M - m0) * lda * 2, 0x7fffffff));
-  const BufRes brsrc = make_res(B + (int64_t)n0 * ldb, min<int64_t>((int64_t)(N - n0) * ldb * 2, 0x7fffffff));
+  const BufRes arsrc =
+      make_res(A + (int64_t)m0 * lda + kbase, min<int64_t>((int64_t)(M - m0) * lda * 2 - kbase * 2, 0x7fffffff));
+  const BufRes brsrc =
+      make_res(B + (int64_t)n0 * ldb + kbase, min<int64_t>((int64_t)(N - n0) * ldb * 2 - kbase * 2, 0x7fffffff));
   int aoff[AL], boff[BL];
   float as[AL];
 #pragma unroll
@@ -443,6 +451,25 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
   // row_ror:8 exchange between lanes l and l ^ 8 then pairs blocks i - 1 and i, so
   // each store instruction writes whole 128-byte rows (8 rows x 64 columns) and L2
   // writes back exactly y (WRITE_SIZE = y; 64-byte runs had read 1.38 x).
+  if (part) {
+    // raw fp32 sums: acc[i][j][4 q + r] is row wm TM + 32 j + fr, column
+    // wn TN + 32 i + 8 q + 4 fk + r of the tile (N is a multiple of 8)
+    float* const pk = part + (int64_t)ks * M * N;
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int m = m0 + wm * TM + j * 32 + fr;
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + wn * TN + i * 32 + 8 * q + 4 * fk;
+          if (m < M && n < N)
+            *reinterpret_cast<float4*>(pk + (int64_t)m * N + n) =
+                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+        }
+    }
+    return;
+  }
   const int rl = lane & 15, cq = lane >> 4;
   const int cl = ((cq & 1) << 4) | ((cq >> 1) << 3);
 #pragma unroll
@@ -520,6 +547,43 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
       }
     }
   }
+}
+
+// Split-K reduction and epilogue: y = bf16((p_0 + p_1 + ...) * sa[m] * sb[n] +
+// bias[n]) over the fp32 partial sums of gemm_kernel's split blocks, summed in
+// split order (deterministic), with the same fp32 epilogue arithmetic as the
+// unsplit kernel. One thread per 8 consecutive columns of a row.
+template <bool A_BF16>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits,
+                                                            const int32_t* __restrict__ a_exp,
+                                                            const float* __restrict__ a_sinv,
+                                                            const float* __restrict__ b_sinv,
+                                                            const uint16_t* __restrict__ bias,
+                                                            uint16_t* __restrict__ C, int64_t ldc, int M, int N) {
+  const int ng = N >> 3;
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= (int64_t)M * ng) return;
+  const int m = (int)(g / ng), n = (int)(g % ng) * 8;
+  const float* src = part + (int64_t)m * N + n;
+  float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
+  for (int k = 1; k < splits; ++k) {
+    const float* q = src + (int64_t)k * M * N;
+    const float4 a = *reinterpret_cast<const float4*>(q), b = *reinterpret_cast<const float4*>(q + 4);
+    lo.x += a.x; lo.y += a.y; lo.z += a.z; lo.w += a.w;
+    hi.x += b.x; hi.y += b.y; hi.z += b.z; hi.w += b.w;
+  }
+  float sa;
+  if constexpr (A_BF16) sa = ldexp1(-a_exp[m]);
+  else sa = a_sinv[m];
+  const float4 s0 = *reinterpret_cast<const float4*>(b_sinv + n), s1 = *reinterpret_cast<const float4*>(b_sinv + n + 4);
+  uint4 bw = make_uint4(0, 0, 0, 0);
+  if (bias) bw = make_uint4(*reinterpret_cast<const uint32_t*>(bias + n), *reinterpret_cast<const uint32_t*>(bias + n + 2),
+                            *reinterpret_cast<const uint32_t*>(bias + n + 4), *reinterpret_cast<const uint32_t*>(bias + n + 6));
+  const uint4 out = make_uint4(pack_bf16(fmaf(lo.x * sa, s0.x, bf16_lo(bw.x)), fmaf(lo.y * sa, s0.y, bf16_hi(bw.x))),
+                               pack_bf16(fmaf(lo.z * sa, s0.z, bf16_lo(bw.y)), fmaf(lo.w * sa, s0.w, bf16_hi(bw.y))),
+                               pack_bf16(fmaf(hi.x * sa, s1.x, bf16_lo(bw.z)), fmaf(hi.y * sa, s1.y, bf16_hi(bw.z))),
+                               pack_bf16(fmaf(hi.z * sa, s1.z, bf16_lo(bw.w)), fmaf(hi.w * sa, s1.w, bf16_hi(bw.w))));
+  stg16(C + (int64_t)m * ldc + n, out);
 }
 
 // Skinny GEMM for M <= 32 * MB rows of a (decode and small batches). One block
@@ -950,7 +1014,22 @@ int64_t num_cus() {
 // eff x (blocks / whole rounds of 256 blocks) x (M / M rounded up to the tile):
 // larger tiles run faster per CU (eff), but a partial last round of blocks or a
 // mostly empty row of tiles wastes CUs.
-int pick_cfg(int64_t M, int64_t N, bool f16a) {
+// Split K in two (tile configurations, workspace entry points): where a tile
+// configuration leaves at least half the CUs without a tile, K >= 2048 and the
+// fp32 partial sums take at most kSplitPartBytes, two blocks per tile each sum half
+// of K into the workspace and a reduction applies the epilogue (256x4096x4096:
+// 128 tiles of 128x64 -> 256 blocks). The output differs from the unsplit one only
+// by the order of the fp32 additions (exact for integer-valued products).
+constexpr size_t kSplitPartBytes = (size_t)8 << 20;
+int pick_split(int cfg, int64_t M, int64_t N, int64_t K) {
+  if (cfg < 0 || cfg >= kNumCfgs || kCfgs[cfg].skinny || kCfgs[cfg].stream || K < 2048) return 1;
+  const int64_t tiles = cdiv(M, kCfgs[cfg].bm) * cdiv(N, kCfgs[cfg].bn);
+  if (2 * tiles > num_cus() || (size_t)2 * (size_t)M * (size_t)N * 4 > kSplitPartBytes) return 1;
+  return 2;
+}
+
+// K > 0: the caller can split K (pick_split), which the score accounts for.
+int pick_cfg(int64_t M, int64_t N, bool f16a, int64_t K = 0) {
   // decode on fp16 a (a16 given, or tbf16_linear's workspace copy): the direct-to-LDS
   // ring for M <= 128 once N fills every CU with at least 32 b rows (M = 16 / 64 /
   // 128 at K = 2560, N = 10240: 13.3 / 18.2 / 23.0 us against 13.6 / 24.1 / 26.9 for
@@ -970,10 +1049,13 @@ int pick_cfg(int64_t M, int64_t N, bool f16a) {
   float best_score = -1.f;
   for (int i = 0; i < ncand; ++i) {
     const TileCfg& t = kCfgs[cand[i]];
-    const int64_t mt = cdiv(M, t.bm), tiles = mt * cdiv(N, t.bn);
+    const int s = K > 0 ? pick_split(cand[i], M, N, K) : 1;
+    const int64_t mt = cdiv(M, t.bm), tiles = mt * cdiv(N, t.bn) * s;
     const float util = (float)tiles / (float)(cdiv(tiles, kCUs) * kCUs);
     const float mutil = (float)M / (float)(mt * t.bm);
-    const float score = eff[i] * util * mutil;
+    // the partial sums' round trip and the reduction launch: 0.9 (17.3 + ~3 us
+    // against 25.2 us unsplit for 256x4096x4096)
+    const float score = eff[i] * util * mutil * (s > 1 ? 0.9f : 1.0f);
     if (score > best_score) {
       best_score = score;
       best = cand[i];
@@ -985,20 +1067,28 @@ int pick_cfg(int64_t M, int64_t N, bool f16a) {
 template <int BM, int BN, int WM, int WN, int BK, int PF, int NS, bool A_BF16>
 void launch_cfg(bool even, unsigned blocks, const uint16_t* a, int64_t lda, const int32_t* a_exp, const float* a_sinv,
                 const uint16_t* b, int64_t ldb, const float* b_sinv, const uint16_t* bi, uint16_t* c, int64_t ldc,
-                int M, int N, int K, hipStream_t st) {
+                int M, int N, int K, float* part, int splits, hipStream_t st) {
+  const int kt_per = (int)cdiv(cdiv(K, BK), splits);
+  const dim3 grid(blocks, part ? (unsigned)splits : 1u);
   if (even)
-    gemm_kernel<BM, BN, WM, WN, BK, PF, NS, A_BF16, true><<<blocks, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
-                                                                               bi, c, ldc, M, N, K);
+    gemm_kernel<BM, BN, WM, WN, BK, PF, NS, A_BF16, true><<<grid, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
+                                                                             bi, c, ldc, M, N, K, part, kt_per);
   else
-    gemm_kernel<BM, BN, WM, WN, BK, PF, NS, A_BF16, false><<<blocks, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
-                                                                                bi, c, ldc, M, N, K);
+    gemm_kernel<BM, BN, WM, WN, BK, PF, NS, A_BF16, false><<<grid, WM * WN * 64, 0, st>>>(a, lda, a_exp, a_sinv, b, ldb, b_sinv,
+                                                                              bi, c, ldc, M, N, K, part, kt_per);
 }
 
+// part / splits: split K over `splits` blocks per tile (tile configurations only),
+// the fp32 partial sums in part (splits x M x N), then splitk_reduce_kernel.
 template <bool A_BF16>
 int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const float* a_sinv, const void* B,
                 int64_t ldb, const float* b_sinv, const void* bias, void* C, int64_t ldc, int64_t M, int64_t N,
-                int64_t K, hipStream_t st) {
+                int64_t K, hipStream_t st, float* part = nullptr, int splits = 1) {
   const int bm = kCfgs[cfg].bm, bn = kCfgs[cfg].bn;
+  TB_CHECK(splits == 1 || (part != nullptr && splits > 1 && !kCfgs[cfg].skinny && !kCfgs[cfg].stream &&
+                           (int64_t)splits * kCfgs[cfg].bk <= K),
+           "gemm: split K needs a tile configuration, a partial-sum buffer and K >= splits k tiles");
+  if (splits == 1) part = nullptr;
   TB_CHECK(!kCfgs[cfg].skinny || M <= bm, "gemm: configuration %d takes M <= %d", cfg, bm);
   TB_CHECK(!kCfgs[cfg].stream || !A_BF16, "gemm: configuration %d needs fp16 a (tbf16_gemm_f16 or tbf16_linear)", cfg);
   // skinny and stream blocks take `rows` weight rows each: as many as fit (bn)
@@ -1019,8 +1109,9 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
   const auto c = (uint16_t*)C;
   const unsigned g = (unsigned)blocks;
   switch (cfg) {
-#define CFG(BM_, BN_, WM_, WN_, BK_, PF_, NS_) \
-  launch_cfg<BM_, BN_, WM_, WN_, BK_, PF_, NS_, A_BF16>(even, g, a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, ldc, M, N, K, st)
+#define CFG(BM_, BN_, WM_, WN_, BK_, PF_, NS_)                                                                       \
+  launch_cfg<BM_, BN_, WM_, WN_, BK_, PF_, NS_, A_BF16>(even, g, a, lda, a_exp, a_sinv, b, ldb, b_sinv, bi, c, ldc, M, N, K, \
+                                                        part, splits, st)
     case 0: CFG(256, 256, 4, 2, 32, 3, 4); break;
     case 1: CFG(128, 128, 2, 2, 64, 2, 2); break;
     case 2: CFG(64, 64, 2, 2, 64, 2, 2); break;
@@ -1053,6 +1144,12 @@ int launch_gemm(int cfg, const void* A, int64_t lda, const int32_t* a_exp, const
 #undef CFG
   }
   TB_LAUNCH_CHECK("gemm");
+  if (part) {
+    const int64_t groups = M * (N / 8);
+    splitk_reduce_kernel<A_BF16><<<(unsigned)cdiv(groups, 256), 256, 0, st>>>(part, splits, a_exp, a_sinv, b_sinv, bi, c,
+                                                                             ldc, (int)M, (int)N);
+    TB_LAUNCH_CHECK("gemm split-K reduction");
+  }
   return 0;
 }
 
@@ -1096,18 +1193,28 @@ bool quantize_once(int cfg, int64_t K) {
   return c.stream || (!c.skinny && c.bn <= 128 && K >= 1024);
 }
 
-// Workspace of tbf16_linear: the row exponents (int32 (M,)) and, where x is
-// quantised once (`quantize_once`), the row inverse scales (fp32 (M,)) and the
-// scaled fp16 copy of x (M, K), each 256-byte aligned.
+// Workspace of tbf16_linear: the row exponents (int32 (M,)); where x is quantised
+// once (`quantize_once`, unless `fused` asks for the conversion inside the GEMM,
+// which the decode kernel cannot do), the row inverse scales (fp32 (M,)) and the
+// scaled fp16 copy of x (M, K); where K is split (`pick_split`), the fp32 partial
+// sums (splits x M x N). Each part 256-byte aligned.
 struct LinearWs {
-  size_t exps, sinv, x16, bytes;
+  size_t exps, sinv, x16, part, bytes;
+  int splits;
+  bool q16;
 };
-LinearWs linear_ws(int64_t M, int64_t K, int cfg) {
-  LinearWs w{0, 0, 0, align_up((size_t)M * 4, 256)};
-  if (quantize_once(cfg, K)) {
+LinearWs linear_ws(int64_t M, int64_t K, int64_t N, int cfg, bool fused = false) {
+  LinearWs w{0, 0, 0, 0, align_up((size_t)M * 4, 256), 1, false};
+  w.q16 = quantize_once(cfg, K) && !(fused && !kCfgs[cfg].stream);
+  if (w.q16) {
     w.sinv = w.bytes;
     w.x16 = w.sinv + align_up((size_t)M * 4, 256);
-    w.bytes = w.x16 + (size_t)M * (size_t)K * 2;
+    w.bytes = align_up(w.x16 + (size_t)M * (size_t)K * 2, 256);
+  }
+  w.splits = pick_split(cfg, M, N, K);
+  if (w.splits > 1) {
+    w.part = w.bytes;
+    w.bytes = w.part + (size_t)w.splits * (size_t)M * (size_t)N * 4;
   }
   return w;
 }
@@ -1117,24 +1224,25 @@ LinearWs linear_ws(int64_t M, int64_t K, int cfg) {
 int linear_into(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N, int64_t ldw,
                 const float* ws, const void* bias, void* y, int64_t ldy, int t, int l1, int cfg, uint8_t* wsp,
                 bool fused, hipStream_t st) {
-  const LinearWs w = linear_ws(M, K, cfg);
+  const LinearWs w = linear_ws(M, K, N, cfg, fused);
   int32_t* exps = reinterpret_cast<int32_t*>(wsp + w.exps);
-  if (!quantize_once(cfg, K) || (fused && !kCfgs[cfg].stream)) {
+  float* part = w.splits > 1 ? reinterpret_cast<float*>(wsp + w.part) : nullptr;
+  if (!w.q16) {
     if (int rc = launch_row_exps(x, M, K, ldx, t, l1, exps, nullptr, st)) return rc;
-    return launch_gemm<true>(cfg, x, ldx, exps, nullptr, w16, ldw, ws, bias, y, ldy, M, N, K, st);
+    return launch_gemm<true>(cfg, x, ldx, exps, nullptr, w16, ldw, ws, bias, y, ldy, M, N, K, st, part, w.splits);
   }
   // x quantised once (exponents, inverse scales, fp16 rows), then the GEMM on fp16
   // operands: the same fp16 values the fused kernels convert in registers
   float* sinv = reinterpret_cast<float*>(wsp + w.sinv);
   void* x16 = wsp + w.x16;
   if (int rc = launch_quantize_rows(x, M, K, ldx, t, l1, x16, K, sinv, exps, st)) return rc;
-  return launch_gemm<false>(cfg, x16, K, nullptr, sinv, w16, ldw, ws, bias, y, ldy, M, N, K, st);
+  return launch_gemm<false>(cfg, x16, K, nullptr, sinv, w16, ldw, ws, bias, y, ldy, M, N, K, st, part, w.splits);
 }
 }  // namespace
 
 extern "C" size_t tbf16_linear_ws_bytes(int64_t M, int64_t K, int64_t N, int cfg) {
   if (M <= 0 || K < 0 || N <= 0 || cfg >= kNumCfgs) return M > 0 ? (size_t)M * 4 : 0;
-  return linear_ws(M, K, cfg < 0 ? pick_cfg(M, N, true) : cfg).bytes;
+  return linear_ws(M, K, N, cfg < 0 ? pick_cfg(M, N, true, K) : cfg).bytes;
 }
 
 extern "C" int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w16, int64_t N,
@@ -1145,7 +1253,7 @@ extern "C" int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, co
   TB_CHECK(aligned16(workspace), "linear: workspace must be 16-byte aligned");
   TB_CHECK(cfg < kNumCfgs, "bad cfg");
   if (M == 0 || N == 0) return 0;
-  return linear_into(x, M, K, ldx, w16, N, ldw, ws, bias, y, ldy, t, l1, cfg < 0 ? pick_cfg(M, N, true) : cfg,
+  return linear_into(x, M, K, ldx, w16, N, ldw, ws, bias, y, ldy, t, l1, cfg < 0 ? pick_cfg(M, N, true, K) : cfg,
                      static_cast<uint8_t*>(workspace), false, as_stream(stream));
 }
 
@@ -1187,11 +1295,11 @@ extern "C" int tbf16_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t
   if (int rc = check_gemm("linear_noalloc", M, N, K, x, ldx, w16, ldw, ws, bias, y, ldy)) return rc;
   TB_CHECK(cfg < kNumCfgs, "bad cfg");
   if (M == 0 || N == 0) return 0;
-  const int c = cfg < 0 ? pick_cfg(M, N, true) : cfg;
+  const int c = cfg < 0 ? pick_cfg(M, N, true, K) : cfg;
   // where the fp16 copy of x does not fit, a tile configuration converts x inside
   // the GEMM instead (the same output); the decode kernel needs the copy
-  const bool fused = !kCfgs[c].stream && linear_ws(M, K, c).bytes > TBF16_NOALLOC_SCRATCH_BYTES;
-  const size_t need = fused ? linear_ws(M, K, -1).bytes : linear_ws(M, K, c).bytes;
+  const bool fused = !kCfgs[c].stream && linear_ws(M, K, N, c).bytes > TBF16_NOALLOC_SCRATCH_BYTES;
+  const size_t need = linear_ws(M, K, N, c, fused).bytes;
   TB_CHECK(need <= TBF16_NOALLOC_SCRATCH_BYTES,
            "linear_noalloc: %lld x %lld needs %zu workspace bytes, beyond the scratch limit of %d bytes", (long long)M,
            (long long)K, need, TBF16_NOALLOC_SCRATCH_BYTES);
