@@ -78,7 +78,10 @@ int tbf16_quantize_cols_t(const void* x, int64_t R, int64_t K, int64_t ldx, int 
  * With the decode configurations, and with tiles of at most 128 columns at K >=
  * 1024, x is quantised once, as the reference's small-M path does: the row
  * inverse scales and x's scaled fp16 copy go into the workspace too, and the
- * GEMM runs on fp16 operands (the same output as converting x inside it). Replaces linear (tbf16/csrc/gemm_sm75.cu:257-284) and, at
+ * GEMM runs on fp16 operands (the same output as converting x inside it). Where
+ * the tiles would leave half of the CUs idle (K >= 2048, at most 8 MiB of partial
+ * sums), K is split in two: fp32 partial sums go into the workspace and a second
+ * kernel adds them in a fixed order and applies the epilogue. Replaces linear (tbf16/csrc/gemm_sm75.cu:257-284) and, at
  * 2 <= M < 256, quantize_rows + cuBLAS + epilogue (tbf16/ops.py:163-178) without
  * its fp16 intermediate. */
 size_t tbf16_linear_ws_bytes(int64_t M, int64_t K, int64_t N, int cfg);
