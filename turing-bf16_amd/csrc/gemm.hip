@@ -552,7 +552,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(const uint16_t* __res
 // Split-K reduction and epilogue: y = bf16((p_0 + p_1 + ...) * sa[m] * sb[n] +
 // bias[n]) over the fp32 partial sums of gemm_kernel's split blocks, summed in
 // split order (deterministic), with the same fp32 epilogue arithmetic as the
-// unsplit kernel. One thread per 8 consecutive columns of a row.
+// unsplit kernel. One thread per 8 consecutive columns of a row; splits >= 2.
 template <bool A_BF16>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits,
                                                             const int32_t* __restrict__ a_exp,
@@ -565,9 +565,14 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   if (g >= (int64_t)M * ng) return;
   const int m = (int)(g / ng), n = (int)(g % ng) * 8;
   const float* src = part + (int64_t)m * N + n;
+  const int64_t stride = (int64_t)M * N;
+  // split 1's loads go out with split 0's (no round trip between them)
   float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
-  for (int k = 1; k < splits; ++k) {
-    const float* q = src + (int64_t)k * M * N;
+  const float4 a1 = *reinterpret_cast<const float4*>(src + stride), b1 = *reinterpret_cast<const float4*>(src + stride + 4);
+  lo.x += a1.x; lo.y += a1.y; lo.z += a1.z; lo.w += a1.w;
+  hi.x += b1.x; hi.y += b1.y; hi.z += b1.z; hi.w += b1.w;
+  for (int k = 2; k < splits; ++k) {
+    const float* q = src + k * stride;
     const float4 a = *reinterpret_cast<const float4*>(q), b = *reinterpret_cast<const float4*>(q + 4);
     lo.x += a.x; lo.y += a.y; lo.z += a.z; lo.w += a.w;
     hi.x += b.x; hi.y += b.y; hi.z += b.z; hi.w += b.w;
