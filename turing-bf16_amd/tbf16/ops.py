@@ -133,12 +133,27 @@ def _prep_gemm_operands(x2, w16, w_sinv, bias):
     return x2, w16, ws, b, N, Np
 
 
+# tbf16_linear's workspace bytes per (device, M, K, N, cfg): the tile choice inside
+# depends on the device's CU count, so it is asked on the tensors' device, once
+_WS_BYTES: dict = {}
+
+
+def _linear_ws_bytes(device: torch.device, M: int, K: int, N: int) -> int:
+    key = (device.index, M, K, N, _GEMM_CFG)
+    wsb = _WS_BYTES.get(key)
+    if wsb is None:
+        if len(_WS_BYTES) > 4096:
+            _WS_BYTES.clear()
+        with torch.cuda.device(device):
+            wsb = _WS_BYTES[key] = int(lib().tbf16_linear_ws_bytes(M, K, N, _GEMM_CFG))
+    return wsb
+
+
 def _linear(x2, w16, w_sinv, bias, t, l1):
     x2, w16, ws, b, N, Np = _prep_gemm_operands(x2, w16, w_sinv, bias)
     M, Kp = x2.shape
     y = torch.empty((M, Np), device=x2.device, dtype=torch.bfloat16)
-    wsb = int(lib().tbf16_linear_ws_bytes(M, Kp, Np, _GEMM_CFG))
-    work = torch.empty((wsb,), device=x2.device, dtype=torch.uint8)
+    work = torch.empty((_linear_ws_bytes(x2.device, M, Kp, Np),), device=x2.device, dtype=torch.uint8)
     launch("tbf16_linear", x2, ptr(x2), M, Kp, x2.stride(0), ptr(w16), Np, w16.stride(0), ptr(ws), ptr(b), ptr(y),
            y.stride(0), int(t), int(l1), _GEMM_CFG, ptr(work))
     return y if Np == N else y[:, :N]
