@@ -1268,8 +1268,9 @@ extern "C" int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, co
 // the host it is only a stand-in symbol): the device address of this GPU's copy
 // comes from hipGetSymbolAddress, taken once per device with that device current,
 // and is what the kernels get. Every call on one GPU shares the array, and the row
-// pass overwrites exactly the part a call uses before its GEMM reads it, so nothing
-// needs clearing; calls that overlap on one GPU (several streams or threads) race.
+// pass (and, with split K, the GEMM's partial sums) overwrites exactly the parts a
+// call uses before they are read, so nothing needs clearing; calls that overlap on
+// one GPU (several streams or threads) race.
 static __device__ __align__(256) uint8_t scratch[TBF16_NOALLOC_SCRATCH_BYTES];
 
 namespace {
