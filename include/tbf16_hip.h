@@ -191,15 +191,20 @@ int tbf16_attn_fwd(const void* q, const void* k, const void* v, int64_t B, int64
  * 2^(ev_q + G)). dq = bf16(scale * dS K16 * 2^(a-G)), dk = bf16(scale * sum_grp
  * dS^T Q16 * 2^(-a-G)), dv = bf16(sum_grp P^T dO16 * 2^(-ev-G)), all from fp32.
  * *overflow (device int32) receives the bit pattern of the largest magnitude of
- * the gradients in the scaled fp16 domain (dq16, dk16, dv16; +inf if any is not
- * finite); at 65520 and above (bits >= 0x477FF000) they would overflow fp16, the
- * reference's retry condition (tbf16/autograd.py:177-189). exps_out int32 [2] =
- * {e, G}. gate: null, or the overflow word of an earlier call with the same
- * arguments and workspace. A gated call is the reference's retry loop run on the
- * device: it does nothing when that call's maximum was below 65520, else it runs
- * at t_do - 8 r with r the number of retries the reference would take (each
- * retry scales every value by 2^-8, at most 5), writing the same outputs and its
- * own overflow word; no host round trip is needed between the two calls. Inputs are the forward's q, k, v, o16, lse and exps; same shape
+ * the gradients in the scaled fp16 domain (dq16, dk16, dv16 of every query head,
+ * taken before a GQA group is summed, as the reference checks them; +inf if any
+ * is not finite); at 65520 and above (bits >= 0x477FF000) they would overflow
+ * fp16, the reference's retry condition (tbf16/autograd.py:177-189). exps_out
+ * int32 [2] = {e, G}. gate: null, or the overflow word of an earlier call with the
+ * same arguments and workspace. A gated call is the reference's retry loop run on
+ * the device: when that call's maximum was below 65520 it leaves the outputs as
+ * they are and copies the gate's word into its own; else it runs at t_do - 8 r
+ * with r the number of retries the reference would take (each retry scales every
+ * value by 2^-8, at most 5), writing the same outputs and its own overflow word;
+ * no host round trip is needed between the two calls. With GQA (H > Hkv) the
+ * workspace also holds each query head's fp32 dK and dV, summed over the group in
+ * head order (the reference's fp32 _reduce_kv). Inputs are the forward's q, k,
+ * v, o16, lse and exps; same shape
  * rules as the forward (D % 8 == 0, D <= 256); dropout_p and seed as given to
  * the forward (its mask is regenerated: dV from P o Z, dS = P o (Z o dP - delta)
  * with Z = keep / (1 - p)).

@@ -13,7 +13,9 @@ accumulation type) or fp64 (the accuracy reference the reference's tests use).
 How each function is pinned (checked by tests/test_oracle.py):
   pow2_exp / pow2_exp_fused   closed-form invariant amax*2^p in [2^(t-1), 2^t) for
                               every normal bf16 amax, frexp identity, edge table,
-                              the C restatement (oracle/pow2.c) and the golden KAT.
+                              the C restatement (oracle/pow2.c) compared on all
+                              65,536 bf16 patterns at test time (no stored KAT file:
+                              the reference ships none).
   quantize_rows/quantize_cols payload == torch's RNE float->half of the same fp32
                               product; s_inv*scale == 1; brute force on tiny inputs.
   bf16/fp16 rounding          torch CPU RNE casts (library routines) and pow2.c.
@@ -29,8 +31,15 @@ How each function is pinned (checked by tests/test_oracle.py):
                               output rounding they model checked on its own.
   sdpa_ref64 / attn_*         closed forms: q=0 -> prefix mean of V rows, one-hot
                               logits copy a V row; fp64 autograd for gradients.
-  attn_bwd_exponents / retry  closed form of autograd.py:175-189 with an injected
-                              overflowing backward.
+  attn_bwd_exponents / retry  the purpose autograd.py:173-176 states: the G found
+                              by searching for the one that puts the largest scaled
+                              dO head maximum at 2^t_do (fp64, math.frexp), with
+                              GQA-expanded and negative ev; hand-derived cases where
+                              an all-zero dO head enters e through ev_q; the retry
+                              sequence with an injected overflowing backward; the
+                              per-query-head overflow check of the emulation on
+                              dominant-key cases whose dv16 is known in closed form
+                              (per head vs group sum disagreeing both ways).
   fmix32 / dropout_keep       this build's own dropout mask (the reference draws its
                               mask from torch's Philox stream, not comparable bit for
                               bit): the published finalizer value fmix32(1) =
@@ -453,31 +462,33 @@ def sdpa_reference_arith(q, k, v, causal=False, scale=None, v_exp=13, rows=None)
 
 
 def sdpa_bwd_reference_arith(q, k, v, dout, causal=False, scale=None):
-    """The reference's training attention arithmetic (autograd.py:149-193) for one
-    attempt without overflow, restated on any device: prepare_qkv(v_exp=0) copies;
-    the fp16 forward (as sdpa_reference_arith, O / l rounded to fp16 = out16, its
-    lse kept in fp32); G from attn_bwd_exponents; dO16 = fp16(dout 2^(ev_q + G));
-    then what the memory-efficient fp16 backward computes: P = exp(s - lse) in fp32,
-    rounded to fp16 for dV = P^T dO16; dP = dO16 V16^T and delta = rowsum(dO16 o
-    out16) in fp32; dS = P (dP - delta) rounded to fp16 for dQ = scale dS K16 and
-    dK = scale dS^T Q16; each gradient accumulated in fp32 and rounded to fp16
-    (dq16, dk16, dv16), GQA groups summed in fp32 (autograd.py:141-146), then
-    head_scale by 2^(a-G), 2^(-a-G), 2^(-ev-G) into bf16. Returns
-    (out bf16, dq, dk, dv bf16, (a, ev, e, G))."""
+    """The reference's training attention arithmetic (autograd.py:149-193) restated
+    on any device: prepare_qkv(v_exp=0) copies; the fp16 forward (as
+    sdpa_reference_arith, O / l rounded to fp16 = out16, its lse kept in fp32); e
+    and the first G from attn_bwd_exponents; then per attempt dO16 = fp16(dout
+    2^(ev_q + G)) and what the memory-efficient fp16 backward computes: P = exp(s -
+    lse) in fp32, rounded to fp16 for dV = P^T dO16; dP = dO16 V16^T and delta =
+    rowsum(dO16 o out16) in fp32; dS = P (dP - delta) rounded to fp16 for dQ =
+    scale dS K16 and dK = scale dS^T Q16; each gradient accumulated in fp32 and
+    rounded to fp16 per query head (dq16, dk16, dv16). If any of those is not finite
+    the attempt is redone at t_do - 8 (at most 6 attempts, autograd.py:177-189) --
+    the check sees every query head's fp16 gradient before a GQA group is summed in
+    fp32 (autograd.py:141-146, 180-186). The accepted attempt is head_scale'd by
+    2^(a-G), 2^(-a-G), 2^(-ev-G) into bf16. Returns (out bf16, dq, dk, dv bf16,
+    (a, ev, e, G))."""
     dev = q.device
     B, H, Sq, D = q.shape
     Hkv, Sk = k.shape[1], k.shape[2]
     q16, k16, v16, a, ev = prepare_qkv(q.cpu(), k.cpu(), v.cpu(), 0)
     q16, k16, v16 = q16.to(dev), k16.to(dev), v16.to(dev)
     evq = expand_heads(ev, H)
-    e, t_do, G = attn_bwd_exponents(dout.cpu(), evq, D)
+    e, t_do, _ = attn_bwd_exponents(dout.cpu(), evq, D)
     sc = (1.0 / math.sqrt(D)) if scale is None else scale
     qi = torch.arange(Sq, device=dev)
     kj = torch.arange(Sk, device=dev)
     out = torch.empty(B, H, Sq, D, dtype=torch.bfloat16, device=dev)
-    dq = torch.empty(B, H, Sq, D, dtype=torch.bfloat16, device=dev)
-    dk32 = torch.zeros(B, Hkv, Sk, D, dtype=torch.float32, device=dev)
-    dv32 = torch.zeros_like(dk32)
+    # the forward (out16, lse) per head, shared by every attempt
+    fwd = {}
     for b in range(B):
         for h in range(H):
             hk = h // (H // Hkv)
@@ -490,16 +501,41 @@ def sdpa_bwd_reference_arith(q, k, v, dout, causal=False, scale=None):
             l = p.sum(-1, keepdim=True)
             o16 = ((p.half().float() @ V) / l).half()
             out[b, h] = (o16.float() * math.ldexp(1.0, int(evq[b, h]))).bfloat16()
-            lse = m + torch.log(l)
-            do16 = (dout[b, h].float() * math.ldexp(1.0, int(evq[b, h]) + G)).half().float()
-            P = torch.exp(s - lse)
-            dv32[b, hk] += (P.half().float().t() @ do16).half().float()
-            dP = do16 @ V.t()
-            delta = (do16 * o16.float()).sum(-1, keepdim=True)
-            dS = (P * (dP - delta)).half().float()
-            dq16 = ((dS @ K) * sc).half()
-            dk32[b, hk] += ((dS.t() @ Q) * sc).half().float()
-            dq[b, h] = (dq16.float() * math.ldexp(1.0, a - G)).bfloat16()
+            fwd[b, h] = (s, o16, m + torch.log(l))
+
+    def attempt(G):
+        dq16 = torch.empty(B, H, Sq, D, dtype=torch.float16, device=dev)
+        dk32 = torch.zeros(B, Hkv, Sk, D, dtype=torch.float32, device=dev)
+        dv32 = torch.zeros_like(dk32)
+        finite = True
+        for b in range(B):
+            for h in range(H):
+                hk = h // (H // Hkv)
+                Q, K, V = q16[b, h].float(), k16[b, hk].float(), v16[b, hk].float()
+                s, o16, lse = fwd[b, h]
+                do16 = (dout[b, h].float() * math.ldexp(1.0, int(evq[b, h]) + G)).half().float()
+                P = torch.exp(s - lse)
+                dv16 = (P.half().float().t() @ do16).half()
+                dP = do16 @ V.t()
+                delta = (do16 * o16.float()).sum(-1, keepdim=True)
+                dS = (P * (dP - delta)).half().float()
+                dq16[b, h] = ((dS @ K) * sc).half()
+                dk16 = ((dS.t() @ Q) * sc).half()
+                finite &= bool(torch.isfinite(dq16[b, h]).all() and torch.isfinite(dk16).all()
+                               and torch.isfinite(dv16).all())
+                dk32[b, hk] += dk16.float()
+                dv32[b, hk] += dv16.float()
+        return dq16, dk32, dv32, finite
+
+    for _ in range(6):
+        G = t_do - e
+        dq16, dk32, dv32, finite = attempt(G)
+        if finite:
+            break
+        t_do -= 8
+    else:
+        raise FloatingPointError("tbf16 attention backward overflowed fp16 even after rescaling")
+    dq = (dq16.float() * math.ldexp(1.0, a - G)).bfloat16()
     # (with Hkv == H each sum holds one fp16 value, which head_scale scales directly)
     sv = torch.tensor([[math.ldexp(1.0, -int(ev[b, h]) - G) for h in range(Hkv)] for b in range(B)],
                       dtype=torch.float32, device=dev)

@@ -356,3 +356,136 @@ def test_attn_backward_device_retry_in_a_graph(dev):
         torch.cuda.synchronize()
         for n, a, b in zip(("dq", "dk", "dv", "exps"), want, got):
             assert torch.equal(a, b), n
+
+
+# ---- backward exponents and the overflow retry, against the oracle -------------------
+
+@pytest.mark.parametrize("zero_dominates", [True, False])
+def test_attn_bwd_exponents_with_zero_heads(dev, zero_dominates):
+    """e and G with an all-zero dO head and an all-zero V head (GQA, H = 4, Hkv = 2):
+    the zero dO head enters e through its ev_q alone (head_exp 0, attention.py:25),
+    deciding e when its kv head's ev is large and dO small, and not otherwise.
+    Bit-exact against the oracle; gradients finite (and within the fp64 bar when
+    the zero head does not decide e; when it does, the other kv head's dO16 falls
+    into fp16's subnormals, as it does in the reference)."""
+    g = G(61)
+    B, H, Hkv, S, D = 1, 4, 2, 200, 64
+    q = (torch.randn(B, H, S, D, generator=g) * 2).bfloat16()
+    k = (torch.randn(B, Hkv, S, D, generator=g) * 2).bfloat16()
+    v = torch.randn(B, Hkv, S, D, generator=g) * 2.0 ** 10
+    v[:, 1] = 0.0  # kv head 1: ev = frexp(0) = 0
+    v = v.bfloat16()
+    do = torch.randn(B, H, S, D, generator=g) * (2.0 ** -20 if zero_dominates else 2.0 ** -8)
+    do[:, 0 if zero_dominates else 2] = 0.0  # on kv head 0 (ev ~ 11) or 1 (ev 0)
+    do = do.bfloat16()
+    a_o, ev_o = O.attn_exponents(q, k, v, 0)
+    e_o, t_do, G_o = O.attn_bwd_exponents(do, O.expand_heads(ev_o, H), D)
+    zero_term = int(O.expand_heads(ev_o, H)[0, 0 if zero_dominates else 2])
+    assert (e_o == zero_term) == zero_dominates
+    qv, kv, vv, dov = (t.to(dev) for t in (q, k, v, do))
+    o, lse, o16, exps = attention.attn_forward(qv, kv, vv, None, True, None, 0, True, True)
+    assert int(exps[0]) == a_o and torch.equal(exps[2:].cpu().reshape(ev_o.shape), ev_o.int())
+    for mode in ("sync", "device"):
+        dq, dk, dv, ex = ag.attn_backward(qv, kv, vv, o16, lse, dov, exps, None, D ** -0.5, True, check=mode)
+        ag.check_pending(block=True)
+        assert (int(ex[0]), int(ex[1])) == (e_o, G_o), mode
+        assert all(torch.isfinite(t).all() for t in (dq, dk, dv))
+    if not zero_dominates:
+        _, rdq, rdk, rdv = attn_bwd64(qv, kv, vv, dov, True)
+        for n, a, r in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+            assert rel(a, r) < 3e-3, (n, rel(a, r))
+
+
+def _dominant_key_gqa(dev, S, signs, D=64):
+    """One kv head, len(signs) query heads; key 0 takes ~99% of every query's
+    attention and query head h's dO is the constant signs[h], so each head's dv16 of
+    key 0 is S * P * 32 (P = e^12.5 / (e^12.5 + S - 1)) with that sign."""
+    H = len(signs)
+    q = torch.zeros(1, H, S, D)
+    q[..., 0] = 10.0
+    k = torch.zeros(1, 1, S, D)
+    k[0, 0, 0, 0] = 10.0
+    v = torch.randn(1, 1, S, D, generator=G(31))
+    do = torch.ones(1, H, S, D) * torch.tensor(signs, dtype=torch.float32)[None, :, None, None]
+    return tuple(t.bfloat16().to(dev) for t in (q, k, v, do))
+
+
+@pytest.mark.parametrize("S,signs,retries", [(1536, (1, 1), 0), (2304, (1, -1), 1)])
+def test_attn_backward_gqa_retry_per_query_head(dev, S, signs, retries):
+    """GQA overflow decided per query head, as the reference checks each head's
+    dk16 / dv16 before summing the group (tbf16/autograd.py:176-186, 141-146):
+    at S = 1536 each head's dv16 (48.9k) fits fp16 while the group sum (97.7k) does
+    not -- no retry; at S = 2304 each head's 73.1k overflows while +1 and -1 heads
+    cancel -- one retry. G equals the oracle's emulation of the reference (which
+    checks per head), in both retry forms, and dv meets the fp64 bar."""
+    q, k, v, do = _dominant_key_gqa(dev, S, signs)
+    D = q.shape[-1]
+    sc = 1 / math.sqrt(D)
+    o, lse, o16, exps = attention.attn_forward(q, k, v, None, False, sc, 0, True, True)
+    _, _, _, own_dv, (_, _, e_o, G_o) = O.sdpa_bwd_reference_arith(q, k, v, do, causal=False, scale=sc)
+    t_do = 12 - math.ceil(math.log2(D))
+    assert G_o == t_do - e_o - 8 * retries
+    host = ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="sync")
+    devc = ag.attn_backward(q, k, v, o16, lse, do, exps, None, sc, False, check="device")
+    ag.check_pending(block=True)
+    assert (int(host[3][0]), int(host[3][1])) == (e_o, G_o)
+    assert torch.equal(host[3].cpu(), devc[3].cpu())
+    for n, a, b in zip(("dq", "dk", "dv"), host[:3], devc[:3]):
+        assert torch.isfinite(a).all() and np.array_equal(bits(a), bits(b)), n
+    qd, kd, vd = (t.double().requires_grad_() for t in (q, k, v))
+    ke, ve = kd.expand(1, len(signs), S, D), vd.expand(1, len(signs), S, D)
+    (torch.softmax(qd @ ke.transpose(-1, -2) * sc, -1) @ ve).backward(do.double())
+    if sum(signs):
+        assert rel(devc[2], vd.grad) < 3e-3, rel(devc[2], vd.grad)
+
+
+def _f32_bits(x: float) -> int:
+    return int(torch.tensor([x], dtype=torch.float32).view(torch.int32)[0])
+
+
+@pytest.mark.parametrize("gate_value,r", [(65520.0 * 300, 2), (float("inf"), 5), (1000.0, 0)])
+def test_attn_backward_gated_call_retry_count(dev, gate_value, r):
+    """A gated call given an earlier attempt's maximum x runs at t_do - 8 r, r the
+    first count with x 2^(-8 r) < 65520, at most 5 (r = 2 and the cap, which no
+    real first attempt here reaches), equal bit for bit to a direct call at that
+    t_do; with nothing to redo (r = 0) it leaves the outputs as they are and writes
+    the gate's word as its own."""
+    g = G(62)
+    B, H, Hkv, S, D = 1, 4, 2, 160, 64
+    q, k, v = ((torch.randn(B, hh, S, D, generator=g) * 3).bfloat16().to(dev) for hh in (H, Hkv, Hkv))
+    do = (torch.randn(B, H, S, D, generator=g) * 2.0 ** -10).bfloat16().to(dev)
+    sc = D ** -0.5
+    o, lse, o16, exps = attention.attn_forward(q, k, v, None, True, sc, 0, True, True)
+    t_do = 12 - math.ceil(math.log2(D))
+    args = (q, k, v, o16, lse, do, exps, None, sc, True)
+    words = torch.zeros(2, device=dev, dtype=torch.int32)
+    dq, dk, dv, ex, _, ws = ag._attn_backward_once(*args, t_do, overflow=words[0:1])
+    first = [t.clone() for t in (dq, dk, dv, ex)]
+    assert not ag._overflowed(int(words[0]))
+    gate = torch.tensor([_f32_bits(gate_value)], device=dev, dtype=torch.int32)
+    ag._attn_backward_once(*args, t_do, overflow=words[1:2], gate=gate, outs=(dq, dk, dv, ex), ws=ws)
+    want = ag._attn_backward_once(*args, t_do - 8 * r)[:4] if r else first
+    torch.cuda.synchronize()
+    for n, a, b in zip(("dq", "dk", "dv", "exps"), (dq, dk, dv, ex), want):
+        assert torch.equal(a, b), (n, r)
+    assert int(ex[1]) == t_do - 8 * r - int(ex[0])
+    if r == 0:
+        assert int(words[1]) == int(gate[0])
+
+
+def test_sdpa_backward_raises_on_persistent_overflow(dev, monkeypatch):
+    """Device mode through autograd: a non-finite dO overflows every retry, and
+    FloatingPointError comes from the backward() call itself (the end-of-backward
+    check), before the gradients can reach an optimizer step."""
+    monkeypatch.setattr(ag, "CHECK_OVERFLOW", "device")
+    q, k, v, do = _dominant_key_gqa(dev, 256, (1, 1))
+    do[0, 1, 3, 5] = float("inf")
+    qd, kd, vd = (t.clone().requires_grad_() for t in (q, k, v))
+    ag._pending.clear()
+    with pytest.raises(FloatingPointError):
+        ag.sdpa(qd, kd, vd, scale=1 / 8, enable_gqa=True).backward(do)
+    assert ag._pending == []
+    # a clean backward afterwards raises nothing
+    q2 = q.clone().requires_grad_()
+    ag.sdpa(q2, k, v, scale=1 / 8, enable_gqa=True).backward(torch.ones_like(do))
+    assert torch.isfinite(q2.grad).all()

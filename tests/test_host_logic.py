@@ -100,6 +100,49 @@ def test_deferred_check_raises_only_for_a_persistent_overflow():
     assert autograd._pending == []
 
 
+def _sdpa_with_fake_kernels(monkeypatch, mode, persistent):
+    """autograd.sdpa on CPU tensors with the kernel calls replaced: the forward returns
+    zeros, the backward enqueues the overflow words of an attempt and its retry (both
+    overflowing when `persistent`) as a device-mode backward does. Returns q's leaf."""
+    monkeypatch.setattr(autograd, "CHECK_OVERFLOW", mode)
+
+    def fwd(q, k, v, bias, is_causal, scale, v_exp, want_lse=False, want_o16=False, dropout_p=0.0, seed=0):
+        z = torch.zeros_like(q)
+        return z, torch.zeros(q.shape[:3]), z.half(), torch.zeros(2 + k.shape[0] * k.shape[1], dtype=torch.int32)
+
+    def bwd(q, k, v, o16, lse, dout, exps, bias, sc, causal, dropout_p=0.0, seed=0, head_dim=None):
+        words = [0x7F800000, 0x7F800000] if persistent else [0x7F800000, 0x46000000]
+        autograd._pending.append((_Done(), torch.tensor(words, dtype=torch.int32)))
+        return torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v), torch.zeros(2, dtype=torch.int32)
+
+    monkeypatch.setattr(autograd.attention, "attn_forward", fwd)
+    monkeypatch.setattr(autograd, "attn_backward", bwd)
+    autograd._pending.clear()
+    q, k, v = (torch.zeros(1, 2, 16, 64, dtype=torch.bfloat16, requires_grad=True) for _ in range(3))
+    return q, autograd.sdpa(q, k, v, is_causal=True)
+
+
+def test_device_mode_raises_from_the_same_backward(monkeypatch):
+    """Device mode: an overflow that persists through the device-side retry raises
+    FloatingPointError from the backward() call that produced it (an end-of-backward
+    callback checks the words), as the reference's host loop raises inside backward
+    (tbf16/autograd.py:184-189), so an optimizer step never sees those gradients.
+    A retry that fixed the overflow raises nothing; the deferred mode leaves the
+    error to check_pending()."""
+    q, o = _sdpa_with_fake_kernels(monkeypatch, "device", persistent=True)
+    with pytest.raises(FloatingPointError):
+        o.float().sum().backward()
+    assert autograd._pending == []
+    q, o = _sdpa_with_fake_kernels(monkeypatch, "device", persistent=False)
+    o.float().sum().backward()
+    assert q.grad is not None and autograd._pending == []
+    q, o = _sdpa_with_fake_kernels(monkeypatch, "deferred", persistent=True)
+    o.float().sum().backward()
+    assert len(autograd._pending) == 1
+    with pytest.raises(FloatingPointError):
+        autograd.check_pending(block=True)
+
+
 def test_target_exp_matches_oracle():
     for K in (1, 7, 8, 100, 2048, 2560, 4096, 32768, 32769, 65536, 1 << 20):
         assert ops._target_exp(K) == O.target_exp(K)
@@ -120,6 +163,19 @@ def test_convert_train_swaps_class_only():
     tbf16.convert(m, train=True, sdpa=False, force=True)
     assert type(m[0]) is convert.TrainLinear and type(m[2]) is convert.TrainLinear
     assert [id(p) for p in m.parameters()] == p0
+
+
+def test_shared_parameters_counts_each_module_once():
+    """A weight tied between two modules is shared; a module reachable from two
+    parents owns its weight once, so it is not treated as tied (the reference counts
+    owners over the deduplicated module list, tbf16/convert.py:132-136)."""
+    lin = nn.Linear(8, 8)
+    twice = nn.ModuleDict({"a": nn.Sequential(lin), "b": nn.Sequential(lin)})
+    assert convert._shared_parameters(twice) == set()
+    emb, head = nn.Embedding(10, 8), nn.Linear(8, 10, bias=False)
+    head.weight = emb.weight
+    tied = nn.ModuleDict({"emb": emb, "head": head})
+    assert convert._shared_parameters(tied) == {id(emb.weight)}
 
 
 def test_mask_to_bias_shapes():

@@ -373,6 +373,122 @@ def test_attn_bwd_exponents_and_retry():
         O.attn_bwd_retry(e, t_do, lambda g_: True)
 
 
+def _g_by_search(dout, ev_q, t_do):
+    """The G the reference's backward picks, found from what it is for
+    (autograd.py:173-176: "scale [dO 2^ev] by g = 2^G so its max sits at 2^t_do"):
+    the one integer G for which the largest math.frexp exponent of the scaled head
+    maxima amax|dO[b,h]| 2^(ev_q[b,h] + G) is t_do, searched over a wide range in
+    fp64. Heads of zeros scale to zero and take no part."""
+    amax = dout.double().abs().amax(dim=(-2, -1))
+    found = [G for G in range(-400, 400)
+             if max(math.frexp(math.ldexp(float(amax[b, h]), int(ev_q[b, h]) + G))[1]
+                    for b in range(amax.shape[0]) for h in range(amax.shape[1]) if amax[b, h] > 0) == t_do]
+    assert len(found) == 1
+    return found[0]
+
+
+def test_attn_bwd_exponents_put_the_scaled_max_at_t_do():
+    """attn_bwd_exponents against the reference's stated purpose: the largest scaled
+    dO head maximum lands in [2^(t_do - 1), 2^t_do) and no head exceeds it, for
+    per-head magnitudes across the exponent range, negative ev, and GQA (ev_q =
+    expand_heads(ev), each query head using kv head h // (H / Hkv))."""
+    g = torch.Generator().manual_seed(40)
+    for trial in range(12):
+        B, Hkv, group = 1 + trial % 2, 1 + trial % 3, 1 + trial % 4
+        H = Hkv * group
+        mags = torch.randint(-30, 20, (B, H, 1, 1), generator=g).double()
+        do = (torch.randn(B, H, 5, 16, generator=g).double() * torch.exp2(mags)).bfloat16()
+        ev = torch.randint(-12, 14, (B, Hkv), generator=g, dtype=torch.int32)
+        ev_q = O.expand_heads(ev, H)
+        for b in range(B):
+            for h in range(H):
+                assert int(ev_q[b, h]) == int(ev[b, h // group])
+        for D in (64, 128, 256):
+            e, t_do, G = O.attn_bwd_exponents(do, ev_q, D)
+            assert t_do == 12 - math.ceil(math.log2(D)) and G == t_do - e
+            assert G == _g_by_search(do, ev_q, t_do), (trial, D)
+            amax = do.double().abs().amax(dim=(-2, -1)) * torch.exp2((ev_q + G).double())
+            assert float(amax.max()) >= 2.0 ** (t_do - 1) and float(amax.max()) < 2.0 ** t_do
+
+
+def test_attn_bwd_exponents_zero_head_enters_through_ev():
+    """A head of dO that is all zeros has head_exp 0 ("0 for all-zero heads",
+    attention.py:25), so it enters e through its ev_q alone (autograd.py:175), as a
+    head whose maximum were in [0.5, 1): hand-derived cases at D = 128 (t_do = 5).
+    Head 0 is zero, head 1 has amax 3 (frexp exponent 2)."""
+    do = torch.zeros(1, 2, 4, 8)
+    do[0, 1, 2, 3] = -3.0
+    do = do.bfloat16()
+    # ev_q = (7, 2): the zero head decides, e = max(0 + 7, 2 + 2) = 7, G = 5 - 7 = -2;
+    # the non-zero head then scales to 3 * 2^(2 - 2) = 3 < 2^4: below t_do
+    e, t_do, G = O.attn_bwd_exponents(do, torch.tensor([[7, 2]], dtype=torch.int32), 128)
+    assert (e, t_do, G) == (7, 5, -2)
+    # ev_q = (3, 2): the non-zero head decides, e = 4, G = 1, 3 * 2^3 = 24 in [16, 32)
+    e, t_do, G = O.attn_bwd_exponents(do, torch.tensor([[3, 2]], dtype=torch.int32), 128)
+    assert (e, t_do, G) == (4, 5, 1) and G == _g_by_search(do, torch.tensor([[3, 2]]), 5)
+    # the zero head acts exactly like a head of constant 0.75 (frexp exponent 0)
+    stand_in = do.clone()
+    stand_in[0, 0] = 0.75
+    for ev_q in ([[7, 2]], [[3, 2]], [[-5, 0]], [[4, 2]]):
+        evq = torch.tensor(ev_q, dtype=torch.int32)
+        assert O.attn_bwd_exponents(do, evq, 128) == O.attn_bwd_exponents(stand_in, evq, 128)
+    # all heads zero: e = max(ev_q)
+    assert O.attn_bwd_exponents(torch.zeros(1, 3, 2, 8).bfloat16(),
+                                torch.tensor([[-4, -9, -6]], dtype=torch.int32), 64) == (-4, 6, 10)
+
+
+def _dominant_key(S, D, do_signs):
+    """Key 0 takes ~99% of every query's attention (logit 12.5 against 0) and each
+    query head's dO is a constant +-1, so dO16 = 2^(t_do - 1) = 32 at D = 64 and
+    dv16 of key 0 is S * P * 32 per query head, with sign do_signs[h] (one kv head)."""
+    H = len(do_signs)
+    q = torch.zeros(1, H, S, D)
+    q[..., 0] = 10.0
+    k = torch.zeros(1, 1, S, D)
+    k[0, 0, 0, 0] = 10.0
+    v = torch.randn(1, 1, S, D, generator=torch.Generator().manual_seed(31))
+    do = torch.ones(1, H, S, D) * torch.tensor(do_signs, dtype=torch.float32)[None, :, None, None]
+    return tuple(t.bfloat16() for t in (q, k, v, do))
+
+
+@pytest.mark.parametrize("S,signs,retries", [(1536, (1, 1), 0), (2304, (1, -1), 1), (2304, (1,), 1),
+                                             (1536, (1,), 0)])
+def test_reference_bwd_retry_checks_each_query_head(S, signs, retries):
+    """The emulation retries on each query head's fp16 gradient, before the GQA group
+    sum: dv16 of key 0 is S * P * 32 with P = e^12.5 / (e^12.5 + S - 1) (logit
+    12.5 against S - 1 zeros). At S = 1536 each head's 48.9k fits fp16 while two
+    heads sum to 97.7k (no retry); at S = 2304 each head's 73.1k overflows while a
+    +1 and a -1 head cancel (one retry, G lowered by 8)."""
+    p0 = math.exp(12.5) / (math.exp(12.5) + S - 1)
+    assert (S * p0 * 32 >= 65520) == (retries == 1)
+    q, k, v, do = _dominant_key(S, 64, signs)
+    _, _, _, dv, (a, ev, e, G) = O.sdpa_bwd_reference_arith(q, k, v, do, causal=False)
+    e0, t_do, G0 = O.attn_bwd_exponents(do, O.expand_heads(ev, len(signs)), 64)
+    assert e == e0 and G == G0 - 8 * retries
+    want = sum(signs) * S * p0  # dv of key 0 per element of dO's constant row
+    assert torch.isfinite(dv).all() and abs(float(dv[0, 0, 0, 0]) - want) <= 0.01 * abs(want) + 1e-3
+
+
+def test_ref64_attn_bwd64_matches_autograd_reference():
+    """tests/_ref64.attn_bwd64 (the hand-written fp64 gradient the GPU tests hold
+    configs[4] against) equals the finite-difference-pinned fp64 autograd of
+    O.sdpa_grads_ref64, causal and not, with GQA (summed per kv head)."""
+    from _ref64 import attn_bwd64
+    g = torch.Generator().manual_seed(41)
+    for H, Hkv, causal in ((2, 2, True), (4, 2, True), (3, 1, False)):
+        q = torch.randn(2, H, 9, 8, generator=g).double()
+        k = torch.randn(2, Hkv, 9, 8, generator=g).double()
+        v = torch.randn(2, Hkv, 9, 8, generator=g).double()
+        do = torch.randn(2, H, 9, 8, generator=g).double()
+        o, dq, dk, dv = attn_bwd64(q, k, v, do, causal)
+        ke, ve = O.expand_heads(k, H), O.expand_heads(v, H)
+        ro, rdq, rdk, rdv = O.sdpa_grads_ref64(q, ke, ve, do, causal=causal)
+        rdk = rdk.view(2, Hkv, H // Hkv, 9, 8).sum(2)
+        rdv = rdv.view(2, Hkv, H // Hkv, 9, 8).sum(2)
+        for a, b in ((o, ro), (dq, rdq), (dk, rdk), (dv, rdv)):
+            assert torch.allclose(a, b, rtol=1e-10, atol=1e-12)
+
+
 def test_attention_grads_fp64_against_finite_difference():
     """The fp64 autograd reference itself: a directional finite difference."""
     g = torch.Generator().manual_seed(10)

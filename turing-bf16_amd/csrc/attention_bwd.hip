@@ -18,14 +18,15 @@
 // r the retries the reference would take: all values scale by exactly 2^-8 per
 // retry, so r follows from the earlier maximum. A gated launch skips prep (q16,
 // k16, v16 and e are already in the workspace and exps_out) and its other kernels
-// return at once when r = 0, so the retry needs no host round trip.
+// return at once when r = 0 (its overflow word then repeats the gate's), so the
+// retry needs no host round trip.
 //
 // Kernels (4 waves, v_mfma_f32_32x32x16_f16):
 //   prep:    q16, k16, v16 (one launch, memory-bound); its first block derives e, G.
 //   delta:   one 16-lane group per query row; also writes dO16.
-//   dkdv:    block = 128 keys (32 per wave, K16 fragments in registers, V16 rows in
-//            per-wave LDS), loops over 64-query tiles (and over the query heads
-//            of a GQA group). Q and dO tiles sit in LDS row-major: the A operand
+//   dkdv:    block = 128 keys of one query head's dK / dV (32 keys per wave, K16
+//            fragments in registers, V16 rows in per-wave LDS), loops over
+//            32-query tiles. Q and dO tiles sit in LDS row-major: the A operand
 //            of S = Q K^T and dP = dO V^T (accumulators: each lane ONE key, 16
 //            queries), and via ds_read_b64_tr_b16 the transposed B operand of
 //            dV += P^T dO and dK += dS^T Q, so P / dS feed the MFMAs straight
@@ -34,6 +35,11 @@
 //            LDS), loops over 64-key tiles: K and V row-major in LDS; S^T and dP^T
 //            give each lane ONE query, and dQ^T += K^T dS^T takes K^T fragments
 //            from ds_read_b64_tr_b16.
+//   kv_reduce (GQA only): with H > Hkv, dkdv writes each query head's dK / dV in
+//            fp32 and this pass sums a group's heads in head order and rounds once
+//            to bf16 (the reference's fp32 _reduce_kv, tbf16/autograd.py:141-146),
+//            so the overflow check sees every query head's dk16 / dv16 before the
+//            sum, as the reference checks its per-head fp16 gradients.
 #include <algorithm>
 #include <math.h>
 
@@ -75,6 +81,8 @@ struct BwdParams {
   int32_t* overflow;      // largest fp16 intermediate magnitude (float bits), this attempt
   const int32_t* gate;    // null, or an earlier attempt's `overflow` word (see above)
   uint16_t *dq, *dk, *dv;
+  // GQA (H > Hkv): per-query-head fp32 dK / dV (B, H, Sk, D), summed by kv_reduce
+  float *dk_part, *dv_part;
   // dropout of the forward pass (DROP kernels regenerate its keep mask)
   uint32_t drop_lo, drop_hi, drop_thr;
   float drop_scale;
@@ -189,7 +197,12 @@ __global__ __launch_bounds__(NTH) void prep_kernel(BwdParams p) {
 // ---- delta = rowsum(dO16 * O16), and dO16 ------------------------------------------
 // One 16-lane group per padded query row; G comes from the prep pass.
 __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
-  if (gated_off(p)) return;
+  if (gated_off(p)) {
+    // nothing to redo: the outputs are the earlier attempt's, and so is this
+    // call's overflow word (below 65520)
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *p.overflow = *p.gate;
+    return;
+  }
   // a gated retry (no prep launch): G at the retried t_do from the first attempt's
   // e; block (0, 0) publishes it for the MFMA kernels and clears the overflow word
   int G;
@@ -228,9 +241,9 @@ __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
 }
 
 // ---- dK, dV --------------------------------------------------------------------
-// Block = 128 keys (32 per wave, K16 fragments in registers, the wave's V16 rows
-// in a private LDS region), loop over 32-query tiles (and over the query heads of
-// a GQA group), double-buffered in LDS by direct global -> LDS loads. Q16 and
+// Block = 128 keys of one query head (32 per wave, K16 fragments in registers, the
+// wave's V16 rows in a private LDS region), loop over 32-query tiles,
+// double-buffered in LDS by direct global -> LDS loads. Q16 and
 // dO16 tiles sit in LDS once, row-major: they are the A operand of S = Q K^T and
 // dP = dO V^T (lane = ONE key, 16 queries), and their transposes for dV += P^T dO
 // and dK += dS^T Q come from ds_read_b64_tr_b16, so P and dS feed the MFMAs
@@ -241,6 +254,9 @@ __global__ __launch_bounds__(NTH) void delta_kernel(BwdParams p) {
 // PART 2 dK, in two launches that each recompute S.
 // DROP: the forward's dropout mask regenerated from (seed, row, key): dV takes
 // P o Z and dS = P o (Z o dP - delta), Z = keep / (1 - p).
+// GQA: the block's query head h reads kv head h / (H / Hkv) and writes its scaled
+// fp32 dK / dV to dk_part / dv_part; kv_reduce sums the group. The block's overflow
+// maximum is then one query head's, as the reference checks dk16 / dv16 per head.
 template <int DP, bool CAUSAL, bool HAS_BIAS, int PART, bool DROP>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(HAS_BIAS || DROP || DP > 128 ? 1 : 2,
                                                                      HAS_BIAS || DROP || DP > 128 ? 1 : 2))) void
@@ -267,9 +283,10 @@ dkdv_kernel(BwdParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, fr = lane & 31, fk = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // grid (heads, key blocks): dispatch runs over heads first, so every head's
-  // heaviest key blocks (the most query tiles under a causal mask) go out first
-  const int bk = blockIdx.x, b = bk / p.Hkv, hk = bk % p.Hkv;
+  // grid (query heads, key blocks): dispatch runs over heads first, so every
+  // head's heaviest key blocks (the most query tiles under a causal mask) go out first
+  const int bh = blockIdx.x, b = bh / p.H, h = bh % p.H;
+  const int bk = b * p.Hkv + h / (p.H / p.Hkv);  // the kv head
   const int k0 = blockIdx.y * BK;
   const int a = p.exps_fwd[0];
   const int ev = p.exps_fwd[2 + bk];
@@ -301,10 +318,9 @@ dkdv_kernel(BwdParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dv[i][r] = 0.f;
 
-  const int group = p.H / p.Hkv;
   const int nqt = (p.Sq + BQ - 1) / BQ;
   const int qt0 = CAUSAL ? min(k0 / BQ, nqt) : 0;
-  const int total = group * (nqt - qt0);
+  const int total = nqt - qt0;
 
   // Query tiles of 32 rows in two LDS stages (tile it in stage it % 2). When tile
   // it starts, threads < 32 load tile it + 1's lse and delta into registers (for
@@ -322,14 +338,8 @@ dkdv_kernel(BwdParams p) {
   }
   float rl = INFINITY, rdl = 0.f;
   uint32_t rdr = 0u;
-  auto tile_src = [&](int it, int& bh, int& q0) {
-    const int h = hk * group + it / (nqt - qt0);
-    q0 = (qt0 + it % (nqt - qt0)) * BQ;
-    bh = b * p.H + h;
-  };
   auto gload = [&](int it, uint8_t* stage) {
-    int bh, q0;
-    tile_src(it, bh, q0);
+    const int q0 = (qt0 + it) * BQ;
     if (tid < BQ) {
       const int qi = q0 + tid;
       rl = qi < p.Sq ? p.lse[(int64_t)bh * p.Sq + qi] : INFINITY;
@@ -359,7 +369,7 @@ dkdv_kernel(BwdParams p) {
   wait_vmem();
   __syncthreads();
   auto tile = [&](int it, const uint8_t* sQ, uint8_t* snext, int stg) {
-    const int q0 = (qt0 + it % (nqt - qt0)) * BQ;
+    const int q0 = (qt0 + it) * BQ;
     const uint8_t* sD = sQ + TILE;
     const bool more = it + 1 < total;
     if (more) gload(it + 1, snext);
@@ -367,7 +377,6 @@ dkdv_kernel(BwdParams p) {
     const bool edge = q0 + BQ > p.Sq || k0 + BK > p.Sk || (CAUSAL && k0 + wave * 32 + 31 >= q0);
     // with a bias the logits are scaled and biased first, as in the forward pass
     const float cs = HAS_BIAS ? 1.f : p.scale_log2;
-    const int h = hk * group + it / (nqt - qt0);
     // S and dP for the tile's 32 queries: lane = one key, 16 queries
     floatx16 sacc, pacc;
 #pragma unroll
@@ -515,19 +524,47 @@ dkdv_kernel(BwdParams p) {
     }
     __syncthreads();
     uint16_t* out = kind == 0 ? p.dv : p.dk;
+    float* part = kind == 0 ? p.dv_part : p.dk_part;  // GQA: this query head's fp32 share
     for (int i = tid; i < 64 * (DP / 8); i += NTH) {
       const int kl = i / (DP / 8), d = (i % (DP / 8)) * 8;
       const int kk = k0 + half * 64 + kl;
       if (kk < p.Sk && d < p.D) {
         const float* src = sOut + kl * DP + d;
-        stg16(out + ((int64_t)bk * p.Sk + kk) * p.D + d,
-              make_uint4(pack_bf16(src[0], src[1]), pack_bf16(src[2], src[3]), pack_bf16(src[4], src[5]),
-                         pack_bf16(src[6], src[7])));
+        if (part) {
+          float* dst = part + ((int64_t)bh * p.Sk + kk) * p.D + d;
+          *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
+          *reinterpret_cast<float4*>(dst + 4) = *reinterpret_cast<const float4*>(src + 4);
+        } else {
+          stg16(out + ((int64_t)bk * p.Sk + kk) * p.D + d,
+                make_uint4(pack_bf16(src[0], src[1]), pack_bf16(src[2], src[3]), pack_bf16(src[4], src[5]),
+                           pack_bf16(src[6], src[7])));
+        }
       }
     }
     __syncthreads();
   }
   record_max(p, mx, nonfinite);
+}
+
+// ---- GQA: dK / dV = sum over a group's query heads -------------------------------
+// part: (B, H, Sk, D) fp32, already scaled; out: (B, Hkv, Sk, D) bf16. One thread per
+// 8 elements, the heads added in order g = 0 .. group - 1, one bf16 rounding.
+__global__ __launch_bounds__(NTH) void kv_reduce_kernel(const float* __restrict__ part, uint16_t* __restrict__ out,
+                                                        int group, int64_t per_head, int64_t n8, const int32_t* gate) {
+  if (gate && retries_after(*gate) == 0) return;  // a gated launch with nothing to redo
+  const int64_t i = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (i >= n8) return;
+  const int64_t e = i * 8, bk = e / per_head, r = e % per_head;
+  const float* src = part + bk * group * per_head + r;
+  float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
+  for (int g = 1; g < group; ++g) {
+    const float4 l = *reinterpret_cast<const float4*>(src + g * per_head);
+    const float4 h = *reinterpret_cast<const float4*>(src + g * per_head + 4);
+    lo.x += l.x; lo.y += l.y; lo.z += l.z; lo.w += l.w;
+    hi.x += h.x; hi.y += h.y; hi.z += h.z; hi.w += h.w;
+  }
+  stg16(out + e, make_uint4(pack_bf16(lo.x, lo.y), pack_bf16(lo.z, lo.w), pack_bf16(hi.x, hi.y),
+                            pack_bf16(hi.z, hi.w)));
 }
 
 // ---- dQ --------------------------------------------------------------------------
@@ -728,11 +765,12 @@ dq_kernel(BwdParams p) {
 
 struct BwdWs {
   int64_t nch, Sqp, Skp, DP;
-  size_t off_delta, off_q16, off_do16, off_k16, off_v16, total;
+  size_t off_delta, off_q16, off_do16, off_k16, off_v16, off_dkp, off_dvp, total;
 };
 
 // partial dO maxima | delta (B, H, Sq) fp32 | q16, dO16 (B, H, Sqp, DP) | k16, v16
-// (B, Hkv, Skp, DP), rows padded to a multiple of 128, DP = 64, 128 or 256
+// (B, Hkv, Skp, DP), rows padded to a multiple of 128, DP = 64, 128 or 256 | with
+// GQA only, the per-query-head fp32 dK and dV (B, H, Sk, D)
 BwdWs bwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D) {
   BwdWs w;
   w.nch = head_amax_chunks(B * H, Sq);
@@ -745,13 +783,16 @@ BwdWs bwd_ws(int64_t B, int64_t H, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t 
   w.off_do16 = w.off_q16 + qb;
   w.off_k16 = w.off_do16 + qb;
   w.off_v16 = w.off_k16 + kb;
-  w.total = w.off_v16 + kb;
+  const size_t pb = H > Hkv ? align_up((size_t)(B * H * Sk * D) * 4, 256) : 0;
+  w.off_dkp = w.off_v16 + kb;
+  w.off_dvp = w.off_dkp + pb;
+  w.total = w.off_dvp + pb;
   return w;
 }
 
 template <int DP>
 int launch_bwd_dp(const BwdParams& p, bool causal, bool has_bias, hipStream_t st) {
-  dim3 g_kv((unsigned)(p.B * p.Hkv), (unsigned)cdiv(p.Sk, 128));
+  dim3 g_kv((unsigned)(p.B * p.H), (unsigned)cdiv(p.Sk, 128));
   dim3 g_q((unsigned)(p.B * p.H), (unsigned)cdiv(p.Sq, 128));
 #define LAUNCH(C, HB, DR)                                        \
   if constexpr (DP > 128) {                                      \
@@ -765,6 +806,7 @@ int launch_bwd_dp(const BwdParams& p, bool causal, bool has_bias, hipStream_t st
   }                                                              \
   dq_kernel<DP, C, HB, DR><<<g_q, NTH, 0, st>>>(p);              \
   TB_LAUNCH_CHECK("attn_bwd/dq");
+  // the forms the kernels come in, then (GQA) the group sums of dK and dV
   if (p.drop_thr) {
     if (causal) {
       if (has_bias) { LAUNCH(true, true, true) } else { LAUNCH(true, false, true) }
@@ -777,6 +819,14 @@ int launch_bwd_dp(const BwdParams& p, bool causal, bool has_bias, hipStream_t st
     if (has_bias) { LAUNCH(false, true, false) } else { LAUNCH(false, false, false) }
   }
 #undef LAUNCH
+  if (p.H > p.Hkv) {
+    const int64_t per_head = (int64_t)p.Sk * p.D, n8 = (int64_t)p.B * p.Hkv * per_head / 8;
+    const unsigned nb = (unsigned)cdiv(n8, NTH);
+    kv_reduce_kernel<<<nb, NTH, 0, st>>>(p.dk_part, p.dk, p.H / p.Hkv, per_head, n8, p.gate);
+    TB_LAUNCH_CHECK("attn_bwd/dk_reduce");
+    kv_reduce_kernel<<<nb, NTH, 0, st>>>(p.dv_part, p.dv, p.H / p.Hkv, per_head, n8, p.gate);
+    TB_LAUNCH_CHECK("attn_bwd/dv_reduce");
+  }
   return 0;
 }
 
@@ -837,6 +887,8 @@ extern "C" int tbf16_attn_bwd(const void* q, const void* k, const void* v, const
   p.do16 = reinterpret_cast<uint16_t*>(wsb + w.off_do16);
   p.k16 = reinterpret_cast<uint16_t*>(wsb + w.off_k16);
   p.v16 = reinterpret_cast<uint16_t*>(wsb + w.off_v16);
+  p.dk_part = H > Hkv ? reinterpret_cast<float*>(wsb + w.off_dkp) : nullptr;
+  p.dv_part = H > Hkv ? reinterpret_cast<float*>(wsb + w.off_dvp) : nullptr;
   p.Sqp = (int)w.Sqp; p.Skp = (int)w.Skp; p.DPc = (int)w.DP;
   // q16, k16, v16 and e do not depend on t_do: a gated attempt finds them in the
   // workspace and exps_out, and its delta pass derives G

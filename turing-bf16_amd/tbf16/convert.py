@@ -150,8 +150,10 @@ def _roots(model) -> list:
 
 
 def _shared_parameters(root: nn.Module) -> set:
-    """ids of parameters registered directly on more than one module (tied weights)."""
-    owners = collections.Counter(id(p) for _, p in root.named_parameters(remove_duplicate=False))
+    """ids of parameters registered directly on more than one module (tied weights).
+    Modules are counted once each (root.modules() deduplicates), so a module reachable
+    from two parents does not make its own weight look tied (tbf16/convert.py:132-136)."""
+    owners = collections.Counter(id(p) for m in root.modules() for p in m.parameters(recurse=False))
     return {pid for pid, n in owners.items() if n > 1}
 
 
