@@ -96,8 +96,10 @@ int tbf16_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* w
  * harnesses that forbid hipMalloc). Where x's fp16 copy does not fit in the array,
  * a tile configuration converts x inside the GEMM instead (the same output); M
  * above TBF16_NOALLOC_MAX_ROWS, or a decode-sized call (M <= 128) whose copy does
- * not fit (K beyond ~48k at M = 128), is rejected (TBF16_EINVAL). Calls that overlap on one GPU (concurrent streams or
- * threads) share the array and race. Same arguments and results as tbf16_linear
+ * not fit (K beyond ~48k at M = 128), is rejected (TBF16_EINVAL). The array used is
+ * the current device's, so the stream must belong to the current device (a stream
+ * of another device is rejected). Calls that overlap on one GPU (concurrent streams
+ * or threads) share the array and race. Same arguments and results as tbf16_linear
  * otherwise. */
 #define TBF16_NOALLOC_MAX_ROWS (1 << 20)
 #define TBF16_NOALLOC_SCRATCH_BYTES (12 << 20)

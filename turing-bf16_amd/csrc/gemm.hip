@@ -28,9 +28,12 @@
 //    smaller tiles remain selectable.
 //  - the MFMA's first operand is the b fragment, the second the a fragment, so a
 //    lane's 16 accumulators are four runs of 4 consecutive n for one m. The
-//    epilogue rounds once to bf16, stages the tile rows in LDS and writes each
-//    row as contiguous 16-byte lanes (register-direct 8-byte stores were
-//    written back in partial sectors, ~5x the output bytes).
+//    epilogue applies the scales and bias in fp32 straight from the
+//    accumulators, rounds once to bf16 and regroups lanes with three register
+//    exchanges (v_permlane32_swap, v_permlane16_swap, a DPP row_ror:8), so each
+//    store instruction writes whole 128-byte rows with no LDS round trip or
+//    barrier (plain 8-byte stores from the accumulators were written back in
+//    partial sectors).
 //  - block ids are remapped so that each XCD (8 per chip, round-robin dispatch)
 //    gets a contiguous range of tiles, grouped 8 a-tiles deep for L2 reuse.
 // M <= 64 (decode) uses a separate skinny kernel that splits K across waves
@@ -1301,6 +1304,15 @@ extern "C" int tbf16_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t
   if (int rc = check_gemm("linear_noalloc", M, N, K, x, ldx, w16, ldw, ws, bias, y, ldy)) return rc;
   TB_CHECK(cfg < kNumCfgs, "bad cfg");
   if (M == 0 || N == 0) return 0;
+  // the scratch address is this device's: the stream must run on it
+  hipStream_t st = as_stream(stream);
+  if (st != nullptr) {
+    int cur = -1;
+    hipDevice_t sd = -1;
+    TB_CHECK(hipGetDevice(&cur) == hipSuccess && hipStreamGetDevice(st, &sd) == hipSuccess,
+             "linear_noalloc: cannot query the stream's device");
+    TB_CHECK(sd == cur, "linear_noalloc: the stream belongs to device %d, the current device is %d", (int)sd, cur);
+  }
   const int c = cfg < 0 ? pick_cfg(M, N, true, K) : cfg;
   // where the fp16 copy of x does not fit, a tile configuration converts x inside
   // the GEMM instead (the same output); the decode kernel needs the copy
@@ -1311,7 +1323,7 @@ extern "C" int tbf16_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t
            (long long)K, need, TBF16_NOALLOC_SCRATCH_BYTES);
   uint8_t* wsp = nullptr;
   if (int rc = scratch_ptr(&wsp)) return rc;
-  return linear_into(x, M, K, ldx, w16, N, ldw, ws, bias, y, ldy, t, l1, c, wsp, fused, as_stream(stream));
+  return linear_into(x, M, K, ldx, w16, N, ldw, ws, bias, y, ldy, t, l1, c, wsp, fused, st);
 }
 
 extern "C" int tbf16_linear_exps(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t* exps,

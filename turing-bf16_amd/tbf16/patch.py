@@ -26,7 +26,7 @@ from . import routing
 from .attention import sdpa
 from .ops import prepare_weight, scaled_linear
 
-# Fewer query rows than this (decoding) run attention natively (tbf16/patch.py:165-167).
+# Fewer query rows than this (decoding) run attention natively (tbf16/patch.py:18-20).
 MIN_ROWS = routing.MIN_QUERY_ROWS
 
 

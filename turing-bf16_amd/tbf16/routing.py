@@ -11,7 +11,7 @@ torch in every one of them instead of raising in some:
 
 The routing thresholds are the reference's: attention with fewer than 16 query
 rows (decoding) and head dims above 256 stay native (tbf16/convert.py:29-30,
-83-84; tbf16/patch.py:165-167,199). Beyond them, this build also sends native
+83-84; tbf16/patch.py:18-20,52). Beyond them, this build also sends native
 what its kernels do not compute: a value head dim different from the key's,
 key/value tensors of different shapes, and batch sizes that disagree.
 
