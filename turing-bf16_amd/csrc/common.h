@@ -96,33 +96,48 @@ __device__ __forceinline__ float wave_sum(float v) {
 // L1 accumulates in fp64 and rounds once to fp32, so the exponent is that of the
 // exact sum (the reference's fp32 thread-order sum, small_kernels.cu:42-59, can
 // differ only within one fp32 ulp of a power of two).
+// L1 sum of one 16-byte chunk (8 bf16) in fp64, left to right; row_amax_regs adds
+// its chunks with the same expression.
+__device__ __forceinline__ double l1_chunk(uint4 v) {
+  return (double)fabsf(bf16_lo(v.x)) + (double)fabsf(bf16_hi(v.x)) + (double)fabsf(bf16_lo(v.y)) +
+         (double)fabsf(bf16_hi(v.y)) + (double)fabsf(bf16_lo(v.z)) + (double)fabsf(bf16_hi(v.z)) +
+         (double)fabsf(bf16_lo(v.w)) + (double)fabsf(bf16_hi(v.w));
+}
+__device__ __forceinline__ float max_chunk(uint4 a) {
+  return fmaxf(fmaxf(fmaxf(fabsf(bf16_lo(a.x)), fabsf(bf16_hi(a.x))), fmaxf(fabsf(bf16_lo(a.y)), fabsf(bf16_hi(a.y)))),
+               fmaxf(fmaxf(fabsf(bf16_lo(a.z)), fabsf(bf16_hi(a.z))), fmaxf(fabsf(bf16_lo(a.w)), fabsf(bf16_hi(a.w)))));
+}
+// Four chunks' loads are issued before any is used, so a lane has four 16-byte
+// loads in flight instead of one (a row of K = 6144 is 12 chunks per lane: one at
+// a time, the L1 pass on dY ran at 3.4 TB/s). The L1 sum still adds the chunks in
+// the order lane, lane + 64, ... into one accumulator: the same bits as one chunk
+// per iteration.
 __device__ __forceinline__ float row_amax_wave(const uint16_t* xr, int K, int lane, bool l1) {
   const uint4* p = reinterpret_cast<const uint4*>(xr);
   const int K8 = K >> 3;
+  constexpr int U = 4;
+  int i = lane;
   if (l1) {
     double acc = 0.0;
-    for (int i = lane; i < K8; i += kWave) {
-      uint4 v = p[i];
-      acc += (double)fabsf(bf16_lo(v.x)) + (double)fabsf(bf16_hi(v.x)) + (double)fabsf(bf16_lo(v.y)) +
-             (double)fabsf(bf16_hi(v.y)) + (double)fabsf(bf16_lo(v.z)) + (double)fabsf(bf16_hi(v.z)) +
-             (double)fabsf(bf16_lo(v.w)) + (double)fabsf(bf16_hi(v.w));
+    for (; i + (U - 1) * kWave < K8; i += U * kWave) {
+      uint4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = p[i + u * kWave];
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc += l1_chunk(v[u]);
     }
+    for (; i < K8; i += kWave) acc += l1_chunk(p[i]);
     return (float)wave_sum_d(acc);
   }
   float m0 = 0.f, m1 = 0.f;
-  int i = lane;
-  for (; i + kWave < K8; i += 2 * kWave) {
-    uint4 a = p[i], b = p[i + kWave];
-    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.x)), fabsf(bf16_hi(a.x))), fmaxf(fabsf(bf16_lo(a.y)), fabsf(bf16_hi(a.y)))));
-    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.z)), fabsf(bf16_hi(a.z))), fmaxf(fabsf(bf16_lo(a.w)), fabsf(bf16_hi(a.w)))));
-    m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(bf16_lo(b.x)), fabsf(bf16_hi(b.x))), fmaxf(fabsf(bf16_lo(b.y)), fabsf(bf16_hi(b.y)))));
-    m1 = fmaxf(m1, fmaxf(fmaxf(fabsf(bf16_lo(b.z)), fabsf(bf16_hi(b.z))), fmaxf(fabsf(bf16_lo(b.w)), fabsf(bf16_hi(b.w)))));
+  for (; i + (U - 1) * kWave < K8; i += U * kWave) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = p[i + u * kWave];
+    m0 = fmaxf(m0, fmaxf(max_chunk(v[0]), max_chunk(v[2])));
+    m1 = fmaxf(m1, fmaxf(max_chunk(v[1]), max_chunk(v[3])));
   }
-  if (i < K8) {
-    uint4 a = p[i];
-    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.x)), fabsf(bf16_hi(a.x))), fmaxf(fabsf(bf16_lo(a.y)), fabsf(bf16_hi(a.y)))));
-    m0 = fmaxf(m0, fmaxf(fmaxf(fabsf(bf16_lo(a.z)), fabsf(bf16_hi(a.z))), fmaxf(fabsf(bf16_lo(a.w)), fabsf(bf16_hi(a.w)))));
-  }
+  for (; i < K8; i += kWave) m0 = fmaxf(m0, max_chunk(p[i]));
   return wave_max(fmaxf(m0, m1));
 }
 

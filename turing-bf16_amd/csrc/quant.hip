@@ -25,10 +25,7 @@ __device__ __forceinline__ float row_amax_regs(const uint4 (&v)[kRegChunks], int
     double acc = 0.0;
 #pragma unroll
     for (int c = 0; c < kRegChunks; ++c)
-      if (lane + c * kWave < K8)
-        acc += (double)fabsf(bf16_lo(v[c].x)) + (double)fabsf(bf16_hi(v[c].x)) + (double)fabsf(bf16_lo(v[c].y)) +
-               (double)fabsf(bf16_hi(v[c].y)) + (double)fabsf(bf16_lo(v[c].z)) + (double)fabsf(bf16_hi(v[c].z)) +
-               (double)fabsf(bf16_lo(v[c].w)) + (double)fabsf(bf16_hi(v[c].w));
+      if (lane + c * kWave < K8) acc += l1_chunk(v[c]);
     return (float)wave_sum_d(acc);
   }
   float m = 0.f;  // zero chunks past the row end leave the maximum alone
