@@ -1,6 +1,7 @@
-"""Size-independent properties at the full sizes the benchmark runs (configs[1]'s
-4096^3 GEMM and configs[3]'s 16k causal attention), where the fp64 checks only
-sample rows.
+"""Size-independent properties at the full sizes of the benchmark configs: configs[1]'s
+4096^3 GEMM, configs[2]'s decode linears (M = 1, 16, 64, 255), configs[3]'s 16k
+causal attention (where the fp64 checks only sample rows) and configs[4]'s training
+linear backward.
 
 A power of two moved from an input into its scale leaves the fp16 operands the
 kernels multiply unchanged: scaling a row of x by 2^s shifts that row's exponent
@@ -8,6 +9,9 @@ by -s and must scale its output row by exactly 2^s; scaling a row of w does the
 same for an output column (its inverse scale carries the power); scaling a head of
 v shifts ev by s and must scale that head's output by exactly 2^s; and q 2^r with
 k 2^-r leaves every logit, so the output, bit for bit the same (a shifts by -r).
+In the backward, a power of two on a row of dY moves that row's L1 exponent and
+scales that row of dX; one common to all of dY moves every column exponent of
+dY^T and scales dW.
 No subnormal or overflowing value is involved at these sizes, so "exactly" means
 equal bits. A dropped or misplaced exponent, a scale applied to the wrong row or
 column, or a second rounding in the epilogue breaks these equalities.
@@ -85,3 +89,45 @@ def test_cfg4_16k_head_powers_of_two(dev):
     assert torch.equal(o_qk.view(torch.int16), o.view(torch.int16))
     # the inference entry point (no exponents asked for) gives the same bits
     assert torch.equal(tbf16.sdpa(q, k, v, is_causal=True).view(torch.int16), o.view(torch.int16))
+
+
+@pytest.mark.parametrize("M", W.CFG3_MS)
+def test_cfg3_decode_row_powers_of_two(dev, M):
+    w, xs = W.cfg3_small_m()
+    w, x = w.to(dev), xs[M].to(dev)
+    g = torch.Generator().manual_seed(13)
+    s = torch.randint(-6, 7, (M,), generator=g).float().to(dev)
+    x2f = x.float() * torch.exp2(s)[:, None]
+    x2 = x2f.bfloat16()
+    assert torch.equal(x2.float(), x2f)
+    w16, ws = ops.prepare_weight(w)
+    y = ops.scaled_linear(x, w16, ws)
+    y2 = ops.scaled_linear(x2, w16, ws)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+    assert torch.equal(y2.float(), y.float() * torch.exp2(s)[:, None])
+
+
+def test_cfg5_linear_backward_powers_of_two(dev):
+    from tbf16 import autograd, routing
+    x, w, dy = (t.to(dev) for t in W.cfg5_train_linear())
+    M, N = dy.shape
+    g = torch.Generator().manual_seed(14)
+    s = torch.randint(-6, 7, (M,), generator=g).float().to(dev)
+    u = 5.0
+
+    def grads(dyv):
+        routing.activations.clear()
+        xg, wg = x.clone().requires_grad_(), w.clone().requires_grad_()
+        autograd.linear(xg, wg).backward(dyv)
+        return xg.grad, wg.grad
+
+    dx, dw = grads(dy)
+    dx_rows, _ = grads((dy.float() * torch.exp2(s)[:, None]).bfloat16())
+    _, dw_all = grads((dy.float() * 2.0 ** u).bfloat16())
+    torch.cuda.synchronize()
+    assert torch.isfinite(dx.float()).all() and torch.isfinite(dw.float()).all()
+    # dX row m = dY row m times W: its L1 exponent shifts, the fp16 operand does not
+    assert torch.equal(dx_rows.float(), dx.float() * torch.exp2(s)[:, None])
+    # dW = dY^T X: a power of two common to all of dY moves every column exponent
+    assert torch.equal(dw_all.float(), dw.float() * 2.0 ** u)
