@@ -1,7 +1,7 @@
 """Size-independent properties at the full sizes of the benchmark configs: configs[1]'s
 4096^3 GEMM, configs[2]'s decode linears (M = 1, 16, 64, 255), configs[3]'s 16k
 causal attention (where the fp64 checks only sample rows) and configs[4]'s training
-linear backward.
+linear and attention backward.
 
 A power of two moved from an input into its scale leaves the fp16 operands the
 kernels multiply unchanged: scaling a row of x by 2^s shifts that row's exponent
@@ -11,10 +11,14 @@ v shifts ev by s and must scale that head's output by exactly 2^s; and q 2^r wit
 k 2^-r leaves every logit, so the output, bit for bit the same (a shifts by -r).
 In the backward, a power of two on a row of dY moves that row's L1 exponent and
 scales that row of dX; one common to all of dY moves every column exponent of
-dY^T and scales dW.
-No subnormal or overflowing value is involved at these sizes, so "exactly" means
-equal bits. A dropped or misplaced exponent, a scale applied to the wrong row or
-column, or a second rounding in the epilogue breaks these equalities.
+dY^T and scales dW. In the attention backward, a power of two on dO scales all
+three gradients. (A power on a head of v is not such a property: the dO exponent
+e is a maximum over heads of head_exp(dO) + ev (tbf16/autograd.py:173-176), so it
+moves G, and dO16's fp16 subnormals round differently.)
+The scaled inputs are exact in bf16 (checked) and each property leaves the fp16
+operands the kernels multiply identical, so "exactly" means equal bits. A dropped
+or misplaced exponent, a scale applied to the wrong row or column, or a second
+rounding in the epilogue breaks these equalities.
 """
 import pytest
 import torch
@@ -131,3 +135,22 @@ def test_cfg5_linear_backward_powers_of_two(dev):
     assert torch.equal(dx_rows.float(), dx.float() * torch.exp2(s)[:, None])
     # dW = dY^T X: a power of two common to all of dY moves every column exponent
     assert torch.equal(dw_all.float(), dw.float() * 2.0 ** u)
+
+
+def test_cfg5_attention_backward_powers_of_two(dev):
+    from tbf16 import autograd
+    q, k, v, do = (t.to(dev) for t in W.cfg5_train_attention())
+    u = 5.0
+
+    def grads(dov):
+        qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+        autograd.sdpa(qg, kg, vg, is_causal=True).backward(dov)
+        return qg.grad, kg.grad, vg.grad
+
+    dq, dk, dv = grads(do)
+    dq_u, dk_u, dv_u = grads((do.float() * 2.0 ** u).bfloat16())
+    torch.cuda.synchronize()
+    assert all(torch.isfinite(t.float()).all() for t in (dq, dk, dv))
+    # every gradient is linear in dO: its exponent e moves by u, G by -u, dO16 not
+    for a, b in ((dq_u, dq), (dk_u, dk), (dv_u, dv)):
+        assert torch.equal(a.float(), b.float() * 2.0 ** u)
