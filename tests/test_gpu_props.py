@@ -81,6 +81,8 @@ def test_cfg4_16k_head_powers_of_two(dev):
     o_v, _, _, e_v = attention.attn_forward(q, k, v2, None, True, None, 13)
     torch.cuda.synchronize()
     assert torch.isfinite(o.float()).all()
+    # causal row 0 sees key 0 alone: P = 1, l = 1, so it is v's row 0, bit for bit
+    assert torch.equal(o[:, :, 0].view(torch.int16), v[:, :, 0].view(torch.int16))
     assert torch.equal(e_v[2:], e[2:] + s.flatten().int())  # ev per head
     assert torch.equal(o_v.float(), o.float() * sv)
 
